@@ -1,0 +1,289 @@
+"""Pin the CPU oracle (CPU-only; no GPU).
+
+The oracle is the checker for every GPU parity test, so it is itself checked:
+
+* against the reference's golden vectors (spconv 2.3.8 outputs held by the
+  reference's own test data, extracted to ``tests/golden``): UNet fwd+bwd,
+  SubMConv2d+SparseConv2d pipeline, max/avg pooling incl. dilation and kv=125;
+* against brute-force enumeration of the rulebook on tiny dense grids, for
+  subm / strided / dilated / transposed geometries;
+* against closed-form literals of the reference tests (output sizes,
+  max-pool zero-init quirk) and structural invariants (mask sortedness and
+  stability, Native compaction order, inverse restores the input rows).
+"""
+
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+from oracle_pipeline import build_unet, canonical_order, OTensor, run_pipeline
+
+
+def _close(actual, expected, atol, msg):
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    assert a.shape == e.shape, f"{msg}: shape {a.shape} != {e.shape}"
+    if a.size:
+        err = float(np.abs(a - e).max())
+        assert err <= atol, f"{msg}: max abs err {err:.3e} > atol {atol:.3e}"
+
+
+# ---------------------------------------------------------------------------
+# golden vectors
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("case_id", ["unet3d_float32", "unet3d_float16"])
+def test_oracle_unet_golden(golden, case_id):
+    case = golden("net.pt", case_id)
+    expect = case["expect"]
+    fwd, named = build_unet(case["state_dict"])
+    inp = case["input"]
+    feats = inp["features"].to(torch.float64).clone().requires_grad_(True)
+    x = OTensor(feats, inp["indices"].numpy(), inp["spatial_shape"], inp["batch_size"])
+    out = fwd(x)
+    assert list(out.spatial_shape) == list(expect["out_spatial_shape"])
+    order = canonical_order(out.indices, out.spatial_shape)
+    np.testing.assert_array_equal(out.indices[order], expect["out_indices"].numpy())
+    _close(out.features.detach().numpy()[order], expect["out_features"], expect["atol_out"], "out")
+    inv = np.empty_like(order)
+    inv[order] = np.arange(order.size)
+    out.features.backward(expect["grad_out"].to(torch.float64)[torch.from_numpy(inv)])
+    _close(feats.grad, expect["grad_input"], expect["atol_grad_input"], "grad_input")
+    for k, ginfo in expect["grad_params"].items():
+        _close(named[k].grad, ginfo["grad"], ginfo["atol"], k)
+
+
+@pytest.mark.parametrize("name,case_id", [
+    ("misc.pt", "seq2d_mixed"),
+    ("ext_pool.pt", "avgp3d_subm"),
+    ("ext_pool.pt", "maxp3d_subm"),
+    ("ext_pool.pt", "maxp3d_d2"),
+    ("ext_pool.pt", "maxp3d_k5_kv125"),
+])
+def test_oracle_pipeline_golden(golden, name, case_id):
+    case = golden(name, case_id)
+    expect = case["expect"]
+    out, feats, layers = run_pipeline(case)
+    assert list(out.spatial_shape) == list(expect["out_spatial_shape"])
+    order = canonical_order(out.indices, out.spatial_shape)
+    np.testing.assert_array_equal(out.indices[order], expect["out_indices"].numpy())
+    _close(out.features.detach().numpy()[order], expect["out_features"], expect["atol_out"], "out")
+    inv = np.empty_like(order)
+    inv[order] = np.arange(order.size)
+    out.features.backward(expect["grad_out"].to(torch.float64)[torch.from_numpy(inv)])
+    _close(feats.grad, expect["grad_input"], expect["atol_grad_input"], "grad_input")
+    named = {}
+    for li, layer in enumerate(layers):
+        for k, v in layer.params().items():
+            named[f"{li}.{k}"] = v
+    for k, ginfo in expect["grad_params"].items():
+        _close(named[k].grad, ginfo["grad"], ginfo["atol"], k)
+
+
+# ---------------------------------------------------------------------------
+# brute force on tiny grids
+# ---------------------------------------------------------------------------
+
+def _rand_indices(rng, batch, shape, n):
+    vol = int(np.prod(shape))
+    pts = []
+    for b in range(batch):
+        lin = rng.choice(vol, size=min(n, vol), replace=False)
+        coords = np.stack(np.unravel_index(lin, shape), 1)
+        pts.append(np.concatenate([np.full((coords.shape[0], 1), b), coords], 1))
+    idx = np.concatenate(pts, 0).astype(np.int32)
+    return idx[rng.permutation(idx.shape[0])]
+
+
+def _brute_pairs(idx, shape, ksize, stride, padding, dilation, out_padding, subm, transpose):
+    """Enumerate (k, j, out_coord) directly from the geometric definition."""
+    ndim = len(shape)
+    inputs = {tuple(r): j for j, r in enumerate(idx.tolist())}
+    offs = list(itertools.product(*[range(k) for k in ksize]))
+    if subm:
+        out_shape = list(shape)
+    elif transpose:
+        out_shape = orc.get_deconv_output_size(shape, ksize, stride, padding, dilation, out_padding)
+    else:
+        out_shape = orc.get_conv_output_size(shape, ksize, stride, padding, dilation)
+    pairs = []
+    for j, row in enumerate(idx.tolist()):
+        b, x = row[0], row[1:]
+        for k, off in enumerate(offs):
+            o = []
+            ok = True
+            for d in range(ndim):
+                if subm:
+                    v = x[d] + (ksize[d] // 2) * dilation[d] - off[d] * dilation[d]
+                elif transpose:
+                    v = x[d] * stride[d] - padding[d] + off[d] * dilation[d]
+                else:
+                    num = x[d] + padding[d] - off[d] * dilation[d]
+                    if num < 0 or num % stride[d]:
+                        ok = False
+                        break
+                    v = num // stride[d]
+                if not (0 <= v < out_shape[d]):
+                    ok = False
+                    break
+                o.append(v)
+            if not ok:
+                continue
+            if subm and (b, *o) not in inputs:
+                continue
+            pairs.append((k, j, (b, *o)))
+    return pairs, out_shape
+
+
+GEOMS = [
+    # (shape, ksize, stride, padding, dilation, out_padding, subm, transpose)
+    ([9, 8, 7], [3, 3, 3], [1, 1, 1], [1, 1, 1], [1, 1, 1], [0, 0, 0], True, False),
+    ([9, 8, 7], [3, 1, 5], [1, 1, 1], [0, 0, 0], [2, 1, 1], [0, 0, 0], True, False),
+    ([9, 8, 7], [3, 3, 3], [2, 2, 2], [1, 1, 1], [1, 1, 1], [0, 0, 0], False, False),
+    ([9, 8, 7], [2, 3, 2], [2, 1, 3], [0, 1, 1], [1, 2, 1], [0, 0, 0], False, False),
+    ([6, 5, 7], [3, 3, 3], [2, 2, 2], [1, 1, 1], [1, 1, 1], [1, 0, 1], False, True),
+    ([12, 11], [3, 3], [2, 2], [1, 1], [1, 1], [0, 0], False, False),
+    ([10, 6, 5, 4], [3, 3, 3, 3], [1, 1, 1, 1], [1, 1, 1, 1], [1, 1, 1, 1], [0] * 4, True, False),
+]
+
+
+@pytest.mark.parametrize("gi", range(len(GEOMS)))
+def test_oracle_pairs_brute_force(gi):
+    shape, ksize, stride, padding, dilation, out_padding, subm, transpose = GEOMS[gi]
+    rng = np.random.default_rng(100 + gi)
+    idx = _rand_indices(rng, 2, shape, max(4, int(np.prod(shape)) // 6))
+    pairs, out_shape = _brute_pairs(idx, shape, ksize, stride, padding, dilation, out_padding,
+                                    subm, transpose)
+    kv = int(np.prod(ksize))
+    res = orc.igemm_pairs(idx, 2, shape, ksize, stride, padding, dilation, out_padding, subm,
+                          transpose, True)
+    out_inds, npl, pf, pb = res[0], res[1], res[2], res[3]
+    if subm:
+        out_keys = [tuple(r) for r in idx.tolist()]
+    else:
+        expect_set = sorted({p[2] for p in pairs},
+                            key=lambda c: np.ravel_multi_index(c, [2, *out_shape]))
+        out_keys = [tuple(r) for r in out_inds.tolist()]
+        assert out_keys == expect_set, "output rows must be sorted unique keys"
+    row_of = {c: r for r, c in enumerate(out_keys)}
+    exp_pf = np.full((kv, len(out_keys)), -1, np.int32)
+    exp_pb = np.full((kv, idx.shape[0]), -1, np.int32)
+    for k, j, o in pairs:
+        exp_pf[k, row_of[o]] = j
+        exp_pb[k, j] = row_of[o]
+    np.testing.assert_array_equal(pf, exp_pf)
+    np.testing.assert_array_equal(pb, exp_pb)
+    assert not npl.any()
+    # Native format: per-offset ascending input rows, npl subm quirk
+    n_inds, pair, n_npl = orc.native_pairs(idx, 2, shape, ksize, stride, padding, dilation,
+                                           out_padding, subm, transpose)
+    for k in range(kv):
+        js = [j for (kk, j, o) in pairs if kk == k]
+        cnt = len(js)
+        np.testing.assert_array_equal(pair[0, k, :cnt], np.array(js, np.int32))
+        np.testing.assert_array_equal(pair[1, k, :cnt], exp_pb[k, js])
+        assert (pair[:, k, cnt:] == -1).all()
+        assert n_npl[k] == (cnt if (not subm or k < kv // 2) else 0)
+    # native -> tables round trip equals the igemm tables
+    t_pf, t_pb = orc.native_pair_to_tables(pair, idx.shape[0], len(out_keys), False)
+    np.testing.assert_array_equal(t_pf, exp_pf)
+    np.testing.assert_array_equal(t_pb, exp_pb)
+    # inverse swap restores the input side
+    i_pf, i_pb = orc.native_pair_to_tables(pair, len(out_keys), idx.shape[0], True)
+    np.testing.assert_array_equal(i_pf, exp_pb)
+    np.testing.assert_array_equal(i_pb, exp_pf)
+
+
+def test_oracle_subm_center_is_identity():
+    rng = np.random.default_rng(7)
+    idx = _rand_indices(rng, 3, [16, 16, 16], 300)
+    res = orc.igemm_pairs(idx, 3, [16, 16, 16], [3, 3, 3], [1] * 3, [1] * 3, [1] * 3, [0] * 3,
+                          True, False, False)
+    np.testing.assert_array_equal(res[2][13], np.arange(idx.shape[0], dtype=np.int32))
+    assert res[3] is None  # eval subm: no pair_bwd
+
+
+def test_oracle_masks_sorted_stable():
+    rng = np.random.default_rng(3)
+    kv, n = 27, 5000
+    table = np.where(rng.random((kv, n)) < 0.3, rng.integers(0, n, (kv, n)), -1).astype(np.int32)
+    table[:, :2000] = np.where(rng.random((kv, 1)) < 0.5, 1, -1)  # many ties
+    pms, args = orc.mask_splits(table, orc.split_masks(kv, False))
+    pm, ar = pms[0][:, 0].astype(np.int64) & 0xFFFFFFFF, args[0]
+    bits = np.zeros(n, np.int64)
+    for k in range(kv):
+        bits |= (table[k] >= 0).astype(np.int64) << k
+    expect_order = np.argsort(bits, kind="stable")
+    np.testing.assert_array_equal(ar, expect_order)
+    np.testing.assert_array_equal(pm, bits[expect_order])
+
+
+def test_oracle_masks_multiword_and_split():
+    rng = np.random.default_rng(4)
+    kv, n = 125, 3000
+    table = np.where(rng.random((kv, n)) < 0.1, 1, -1).astype(np.int32)
+    pms, args = orc.mask_splits(table, orc.split_masks(kv, False))
+    words = np.zeros((n, 4), np.int64)
+    for k in range(kv):
+        words[:, k // 32] |= (table[k] >= 0).astype(np.int64) << (k % 32)
+    order = np.lexsort([words[:, w] for w in range(4)])  # last key (word 3) most significant
+    np.testing.assert_array_equal(args[0], order)
+    np.testing.assert_array_equal(pms[0].astype(np.int64) & 0xFFFFFFFF, words[order])
+    m = orc.split_masks(27, True)
+    assert [int(v[0]) for v in m] == [(1 << 14) - 1, ((1 << 13) - 1) << 14]
+    # the unsigned order must survive the int32 wrap: bit 31 set sorts last
+    t2 = np.full((32, 3), -1, np.int32)
+    t2[31, 0] = 5
+    t2[0, 1] = 5
+    pms2, args2 = orc.mask_splits(t2, orc.split_masks(32, False))
+    np.testing.assert_array_equal(args2[0], [2, 1, 0])
+    assert pms2[0][2, 0] == np.int32(-2 ** 31)
+
+
+def test_oracle_output_sizes():
+    f = orc.get_conv_output_size
+    assert f([32, 32, 32], [3, 3, 3], [2, 2, 2], [1, 1, 1], [1, 1, 1]) == [16, 16, 16]
+    assert f([7, 8], [3, 3], [2, 2], [1, 1], [1, 1]) == [4, 4]
+    assert f([24], [3], [1], [2], [2]) == [24]
+    assert f([13, 7], [-1, 3], [1, 1], [0, 0], [1, 1]) == [1, 5]
+    assert f([10], [2], [2], [0], [1]) == [5]
+    g = orc.get_deconv_output_size
+    assert g([16, 16, 16], [2, 2, 2], [2, 2, 2], [0, 0, 0], [1, 1, 1], [0, 0, 0]) == [32, 32, 32]
+    assert g([16], [3], [2], [1], [1], [1]) == [32]
+    with pytest.raises(ValueError):
+        g([8], [-1], [1], [0], [1], [0])
+
+
+def test_oracle_maxpool_zero_init_quirk():
+    idx = np.array([[0, 0, 0, 0], [0, 0, 0, 1], [0, 4, 4, 4], [0, 4, 4, 5]], np.int32)
+    feats = np.array([[-1.0], [-2.0], [3.0], [-0.5]], np.float32)
+    res = orc.igemm_pairs(idx, 1, [8, 8, 8], [2] * 3, [2] * 3, [0] * 3, [1] * 3, [0] * 3, False, False, True)
+    out = orc.maxpool_fwd(feats, res[2])
+    order = np.argsort(res[0][:, 1], kind="stable")
+    np.testing.assert_array_equal(out[order, 0], [0.0, 3.0])
+
+
+def test_oracle_gemm_against_dense_conv():
+    """fp64 gather-GEMM == dense torch conv3d on a tiny fully-occupied grid."""
+    rng = np.random.default_rng(11)
+    S, C, K = 5, 3, 4
+    coords = np.stack(np.meshgrid(*[np.arange(S)] * 3, indexing="ij"), -1).reshape(-1, 3)
+    idx = np.concatenate([np.zeros((coords.shape[0], 1)), coords], 1).astype(np.int32)
+    X = rng.standard_normal((idx.shape[0], C))
+    W = rng.standard_normal((K, 3, 3, 3, C))
+    res = orc.igemm_pairs(idx, 1, [S] * 3, [3] * 3, [1] * 3, [1] * 3, [1] * 3, [0] * 3, True, False, True)
+    out = orc.gemm_fwd(X, W.reshape(K, 27, C), res[2])
+    dense = torch.from_numpy(X.T.reshape(1, C, S, S, S))
+    wt = torch.from_numpy(W).permute(0, 4, 1, 2, 3)  # [K, C, kz, ky, kx]
+    ref = torch.nn.functional.conv3d(dense, wt, padding=1)[0].reshape(K, -1).T.numpy()
+    np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-12)
+    # wgrad / dgrad are the adjoints of fwd: <G, fwd(X, W)> == <dgrad(G), X> == <wgrad(X, G), W>
+    G = rng.standard_normal(out.shape)
+    lhs = float((G * out).sum())
+    dX = orc.gemm_dgrad(G, W.reshape(K, 27, C), res[3])
+    dW = orc.gemm_wgrad(X, G, res[2], K, C)
+    assert abs(lhs - float((dX * X).sum())) < 1e-9 * max(1.0, abs(lhs))
+    assert abs(lhs - float((dW * W.reshape(K, 27, C)).sum())) < 1e-9 * max(1.0, abs(lhs))
