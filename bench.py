@@ -1,0 +1,263 @@
+"""Benchmark of the sparse-convolution hot path on one MI355X.
+
+Workload (BASELINE.json metric): SubMConv3d 3x3x3, 64 -> 64 channels, fp16,
+eval, bias on, Kaiming-uniform weights; input 200k unique voxels of a seeded
+surface-like cloud (sphere shells + plane patches) in a 256^3 grid, batch 1,
+features N(0, 1).  A step is one forward of the layer with its rulebook
+cached under its indice_key (the reference times subm "with the neighborhood
+map cached & reused"); steps are replayed from a HIP graph so the GPU, not the
+Python host, is measured.  Also reported:
+
+* pairgen_ms: cold build of the subm rulebook (hash build + probe + mask sort);
+* eager_ms: the same forward called from Python without a graph;
+* roofline: the gather-GEMM kernel's algorithmic bytes per launch over its
+  average launch time (HIP events on the stream it runs on);
+* cpu_baseline: the CPU oracle (C/OpenMP restatement of the reference
+  algorithm, fp32) on the same layer, on a bounded sample of rows.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT), str(ROOT / "spconv-triton_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+METRIC = "fwd ms + Mvoxels/s, SubMConv3d 64→64 fp16 @200k voxels; pairgen ms; %roofline"
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+N_VOXELS = 200_000
+GRID = 256
+C_IN = C_OUT = 64
+KV = 27
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_layer(torch, spconv, dev):
+    torch.manual_seed(0)
+    conv = spconv.SubMConv3d(C_IN, C_OUT, 3, padding=1, bias=True, indice_key="subm0")
+    return conv.to(dev).half().eval()
+
+
+def gemm_bytes(n_in: int, n_out: int) -> int:
+    """Algorithmic HBM bytes of one forward launch: features read once, output
+    written once, weights once, the dense [kv, n_out] int32 gather table, and
+    the sorted mask word + argsort entry of every output row."""
+    e = 2
+    return e * (n_in * C_IN + n_out * C_OUT + KV * C_IN * C_OUT) + 4 * KV * n_out + 8 * n_out
+
+
+def cpu_baseline(idx, feats_np, w_np, b_np, pf_np):
+    """Oracle forward (fp32) on a bounded row sample; returns the dict for the JSON line."""
+    import numpy as np
+
+    from oracle import oracle as orc
+
+    threads = len(os.sched_getaffinity(0))
+    threads = min(threads, int(os.environ.get("OMP_NUM_THREADS", threads)))
+    orc.set_num_threads(threads)
+    rows = 50_000
+    pf_s = np.ascontiguousarray(pf_np[:, :rows])
+    w = w_np.reshape(C_OUT, KV, C_IN).astype(np.float32)
+    x = feats_np.astype(np.float32)
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        orc.gemm_fwd_f32(x, w, pf_s, b_np.astype(np.float32))
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 10.0 or reps >= 50:
+            break
+    per_row = el / (reps * rows)
+    # the reference's pair generation on the CPU (sort + binary search) for the full cloud
+    t1 = time.perf_counter()
+    orc.igemm_pairs(idx, 1, [GRID] * 3, [3] * 3, [1] * 3, [1] * 3, [1] * 3, [0] * 3, True, False,
+                    False)
+    pairgen_s = time.perf_counter() - t1
+    return {
+        "value": round(1.0 / per_row / 1e6, 4),
+        "unit": "Mvoxels/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle/spconv_oracle.c gemm_fwd_f32 (fp32; the host has no fp16 GEMM) on "
+                   f"{rows} of the {N_VOXELS} output rows x {reps} passes, {threads} OpenMP "
+                   f"threads; oracle sort-based pair generation of the full cloud "
+                   f"{pairgen_s * 1e3:.1f} ms"),
+        "pairgen_ms": round(pairgen_s * 1e3, 2),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the sparse-conv hot path shards by batch sample; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import spconv_triton.pytorch as spconv
+    from bench_data import surface_cloud
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    log("generating the 200k-voxel surface cloud")
+    idx_np = surface_cloud(N_VOXELS, GRID, seed=0)
+    idx = torch.from_numpy(idx_np).to(dev)
+    torch.manual_seed(1)
+    feats = torch.randn(N_VOXELS, C_IN, device=dev).half()
+    conv = build_layer(torch, spconv, dev)
+
+    # ---- cold pair generation -------------------------------------------
+    def pairgen():
+        return ops.get_indice_pairs_implicit_gemm(idx, 1, [GRID] * 3, ConvAlgo.MaskImplicitGemm,
+                                                  [3] * 3, [1] * 3, [1] * 3, [1] * 3, [0] * 3,
+                                                  True, is_train=False)
+
+    log("pair generation")
+    for _ in range(5):
+        res = pairgen()
+    torch.cuda.synchronize()
+    pg = []
+    for _ in range(30):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        res = pairgen()
+        e.record()
+        torch.cuda.synchronize()
+        pg.append(s.elapsed_time(e))
+    pairgen_ms = statistics.median(pg)
+    pf = res[2]
+    n_pairs = int((pf >= 0).sum().item())
+
+    # ---- forward with the rulebook cached --------------------------------
+    with torch.no_grad():
+        x0 = spconv.SparseConvTensor(feats, idx, [GRID] * 3, 1)
+        y0 = conv(x0)  # builds and caches the rulebook under "subm0"
+        xc = spconv.SparseConvTensor(feats, idx, [GRID] * 3, 1, indice_dict=y0.indice_dict)
+        for _ in range(3):
+            y = conv(xc)
+        torch.cuda.synchronize()
+        # eager timing (Python host in the loop)
+        t0 = time.perf_counter()
+        for _ in range(200):
+            y = conv(xc)
+        torch.cuda.synchronize()
+        eager_ms = (time.perf_counter() - t0) / 200 * 1e3
+
+        log("capturing the forward in a HIP graph")
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                conv(xc)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            yg = conv(xc)
+        graph.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(yg.features, y.features):
+            raise RuntimeError("graph replay differs from the eager forward")
+
+        log(f"warmup {args.warmup}, timed {args.steps} steps")
+        for _ in range(args.warmup):
+            graph.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        wall_s = time.perf_counter() - t0
+        ms_per_step = wall_s / args.steps * 1e3
+
+        # kernel-level timing for the roofline: events on the stream the GEMM
+        # kernel runs on (torch's current stream, which the library uses)
+        stream = torch.cuda.current_stream()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 500
+        s.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e.record(stream)
+        torch.cuda.synchronize()
+        kernel_ms = s.elapsed_time(e) / reps
+
+    nbytes = gemm_bytes(N_VOXELS, N_VOXELS)
+    flops = 2.0 * n_pairs * C_IN * C_OUT
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    mvox = N_VOXELS / (ms_per_step * 1e-3) / 1e6
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("CPU baseline (oracle)")
+        w_np = conv.weight.detach().float().cpu().numpy()
+        b_np = conv.bias.detach().float().cpu().numpy()
+        cpu = cpu_baseline(idx_np, feats.float().cpu().numpy(), w_np, b_np, pf.cpu().numpy())
+
+    line = {
+        "metric": METRIC,
+        "value": round(mvox, 2),
+        "unit": "Mvoxels/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {
+            "workload": "SubMConv3d k3 64->64 fp16 eval, 200k-voxel surface cloud in 256^3, "
+                        "batch 1, rulebook cached, HIP-graph replay",
+            "n_voxels": N_VOXELS,
+            "pairs": n_pairs,
+            "parallelism": "single_gpu",
+        },
+        "fwd_ms": round(ms_per_step, 5),
+        "eager_ms": round(eager_ms, 5),
+        "pairgen_ms": round(pairgen_ms, 4),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "gather_gemm<f16,f16,MASK,VEC>",
+            "kernel_ms": round(kernel_ms, 5),
+            "algorithmic_bytes": nbytes,
+            "mfma_tflops": round(flops / (kernel_ms * 1e-3) / 1e12, 2),
+            "mfma_frac": round(flops / (kernel_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,238 @@
+/*
+ * spconv_hip.h -- C ABI of the MI355X (gfx950) sparse-convolution library
+ * libspconv_hip.so.
+ *
+ * Every entry point takes plain device pointers, element counts, small host
+ * structs and a HIP stream (passed as void*, i.e. a hipStream_t), and returns
+ * an int status (SP_OK == 0).  Nothing here allocates device memory: callers
+ * pass a workspace whose size they query first.  All work is enqueued on the
+ * given stream; only sp_pairgen_conv_build() blocks the host, once, to read
+ * the data-dependent output count (the reference synchronises at the same
+ * point: torch.unique in spconv_triton/pytorch/_impl/pairs.py:206-209).
+ *
+ * The reference (spconv-Triton) has no FFI: its boundary is the Python
+ * module spconv_triton/pytorch/_impl/{pairs,pair_kernels,gemm,pool}.py,
+ * called from spconv_triton/pytorch/ops.py.  Each declaration below names the
+ * reference function (file:line, paths relative to the reference repository)
+ * whose result it reproduces.  The Python mirror of that module in this
+ * repository binds these symbols with ctypes.
+ *
+ * Index tensors are int32.  Feature tensors are row-major [rows, channels].
+ * Weights are KRSC, i.e. [K_out, kv, C_in] contiguous
+ * (spconv_triton/pytorch/ops.py:76-83).
+ */
+#ifndef SPCONV_HIP_H
+#define SPCONV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define SP_OK 0
+#define SP_ERR_INVALID_ARG 1  /* bad size / null pointer / misaligned table */
+#define SP_ERR_UNSUPPORTED 2  /* dtype or shape the library does not handle */
+#define SP_ERR_WORKSPACE 3    /* workspace smaller than the queried size */
+#define SP_ERR_HIP 4          /* a HIP runtime call failed */
+#define SP_ERR_HASH_FULL 5    /* coordinate hash overflowed its capacity */
+
+/* ---- element types ----------------------------------------------------- */
+#define SP_F16 0
+#define SP_BF16 1
+#define SP_F32 2
+#define SP_F64 3
+
+/* ---- pair-generation modes (spconv_triton/pytorch/_impl/pairs.py:6-22) -- */
+#define SP_PAIR_SUBM 0       /* o = x + (k//2)*d - kpos*d, o must be an input */
+#define SP_PAIR_REGULAR 1    /* o = (x + p - kpos*d) / s, exact division     */
+#define SP_PAIR_TRANSPOSE 2  /* o = x*s - p + kpos*d                         */
+
+/* Convolution geometry, host memory.  ndim in 1..4.  For SP_PAIR_SUBM the
+ * library derives padding = (ksize//2)*dilation and stride 1 itself
+ * (pairs.py:186-191); out_shape must equal in_shape. */
+typedef struct sp_geom {
+  int32_t ndim;
+  int32_t mode;
+  int64_t batch_size;
+  int64_t in_shape[4];
+  int64_t out_shape[4];
+  int32_t ksize[4];
+  int32_t stride[4];
+  int32_t padding[4];
+  int32_t dilation[4];
+} sp_geom;
+
+/* ---- library info ------------------------------------------------------ */
+int sp_version(void);              /* (major << 16) | (minor << 8) | patch */
+const char* sp_arch(void);         /* offload target the code objects hold */
+const char* sp_last_error(void);   /* message of the last failing call (thread-local) */
+
+/* 1 when the key volume needs 64-bit linear keys: batch*prod(out_shape)
+ * (and, for subm, batch*prod(in_shape)) >= 2^31.
+ * Replaces the lin_dtype pick of compute_candidates, pairs.py:166-171. */
+int sp_geom_key64(const sp_geom* g);
+
+/* ---- pair generation --------------------------------------------------- */
+
+/* Workspace bytes for sp_pairgen_subm / sp_pairgen_conv_build+fill on n input
+ * rows.  The same workspace must be passed, untouched, from build to fill. */
+size_t sp_pairgen_workspace_size(const sp_geom* g, int64_t n);
+
+/* Submanifold rulebook.  pair_fwd [kv, n] (nullable if pair_bwd is given):
+ * pair_fwd[k, r] = input row j whose coordinate is the k-th neighbour of row
+ * r, or -1.  pair_bwd [kv, n]
+ * (nullable) is the transposed table, pair_bwd[k, j] = r or -1.  mask_words
+ * [n, ceil(kv/32)] (nullable): bit k%32 of word k/32 set iff pair_fwd[k,r]>=0.
+ * Reproduces compute_candidates(subm) + scatter_igemm_pairs + pack_mask_words:
+ *   spconv_triton/pytorch/_impl/pairs.py:126-204, :318-340
+ *   spconv_triton/pytorch/_impl/pair_kernels.py:37-94, :159-183, :220-261, :398-446 */
+int sp_pairgen_subm(const sp_geom* g, const int32_t* indices, int64_t n,
+                    int32_t* pair_fwd, int32_t* pair_bwd, uint32_t* mask_words,
+                    void* ws, size_t ws_bytes, void* stream);
+
+/* Regular / transposed convolution, phase 1: deduplicate the candidate output
+ * keys, sort them ascending (batch-major linear key), and rank them.  Blocks
+ * until the count is known and stores it in *n_out (0 = every point vanished).
+ * Replaces K1 + out_lin[valid] + torch.unique + K3 of
+ *   spconv_triton/pytorch/_impl/pairs.py:126-220 (regular/transpose branch)
+ *   spconv_triton/pytorch/_impl/pair_kernels.py:37-94, :298-392 */
+int sp_pairgen_conv_build(const sp_geom* g, const int32_t* indices, int64_t n,
+                          void* ws, size_t ws_bytes, int64_t* n_out, void* stream);
+
+/* Phase 2: output coordinates and gather tables for the first n_keep outputs
+ * (n_keep <= n_out; smaller values implement num_out_act_bound,
+ * pairs.py:318-323).  out_indices [n_keep, ndim+1]; pair_fwd [kv, n_keep]
+ * (nullable if pair_bwd is given);
+ * pair_bwd [kv, n] (nullable); mask_words_bwd [n, ceil(kv/32)] (nullable).
+ * Replaces _delinearize + scatter_igemm_pairs, pairs.py:98-111, :318-340,
+ * pair_kernels.py:220-261. */
+int sp_pairgen_conv_fill(const sp_geom* g, const int32_t* indices, int64_t n,
+                         const void* ws, size_t ws_bytes, int64_t n_keep,
+                         int32_t* out_indices, int32_t* pair_fwd, int32_t* pair_bwd,
+                         uint32_t* mask_words_bwd, void* stream);
+
+/* Per-row offset bitmask of a gather table [kv, n] -> words [n, ceil(kv/32)].
+ * Replaces pack_mask_words, spconv_triton/pytorch/_impl/pair_kernels.py:147-213. */
+int sp_mask_words(const int32_t* table, int64_t kv, int64_t n, uint32_t* words,
+                  void* stream);
+
+/* Mask split + stable sort of mask words (make_mask_splits, pairs.py:356-392).
+ * words [n, mic]; word 0 is ANDed with split_mask.  With do_sort, rows are
+ * stably sorted ascending by the unsigned value, the highest word most
+ * significant.  pair_mask [n, mic] (int32, wrapped) receives the sorted
+ * words, argsort [n] the original row of each sorted entry. */
+size_t sp_mask_sort_workspace_size(int64_t n, int32_t mic);
+int sp_mask_sort(const uint32_t* words, int64_t n, int32_t mic, int32_t kv,
+                 uint32_t split_mask, int32_t do_sort, int32_t* pair_mask,
+                 int32_t* argsort, void* ws, size_t ws_bytes, void* stream);
+
+/* Per-row compaction of a table [kv, n]: for every k, the columns i with
+ * table[k, i] >= 0 in ascending order go to pos_out[k, p] = i and
+ * val_out[k, p] = table[k, i]; the tail of each row is filled with -1.
+ * counts[k] = number of entries; npl[k] = counts[k] for k < npl_limit, else 0
+ * (npl nullable).  Serves the Native [2, kv, N] format (pos = input rows,
+ * val = output rows: _scatter_pairs_native + native_pairs, pairs.py:223-278)
+ * and the compacted weight-gradient signal (gemm.py:661-669). */
+size_t sp_compact_workspace_size(int64_t kv, int64_t n);
+int sp_compact_table(const int32_t* table, int64_t kv, int64_t n, int32_t* pos_out,
+                     int32_t* val_out, int32_t* counts, int32_t* npl, int32_t npl_limit,
+                     void* ws, size_t ws_bytes, void* stream);
+
+/* Native pair tensor [2, kv, n_pairs] -> gather tables.  pf [kv, n_out]
+ * (-1 filled), pb [kv, n_in] (nullable).  inverse swaps the two rows of the
+ * pair tensor.  Replaces native_pair_to_tables, pairs.py:429-469. */
+int sp_native_to_tables(const int32_t* pair, int64_t kv, int64_t n_pairs, int32_t inverse,
+                        int64_t n_in, int64_t n_out, int32_t* pf, int32_t* pb,
+                        void* stream);
+
+/* ---- gather-GEMM ------------------------------------------------------- */
+
+/* Workspace for sp_conv_fwd / sp_conv_dgrad (relaid weights + fp32 bias). */
+size_t sp_conv_workspace_size(int64_t K, int64_t kv, int64_t C, int32_t dtype);
+
+/* Pre-packed weights: the KRSC weight (and optional bias) relaid once into the
+ * MFMA operand layout of `dtype`, for the forward (transpose = 0, output
+ * channels K) or the input gradient (transpose = 1, output channels C).  A
+ * packed buffer stays valid while the weight is unchanged, so inference runs
+ * the gather-GEMM as a single kernel launch.  Same computation as the weight
+ * handling inside conv_forward / conv_backward_input, gemm.py:501-631. */
+size_t sp_conv_packed_bytes(int64_t K, int64_t kv, int64_t C, int32_t dtype, int32_t transpose);
+int sp_conv_pack_weight(const void* w, int32_t w_dtype, const void* bias, int64_t K, int64_t kv,
+                        int64_t C, int32_t dtype, int32_t transpose, void* packed,
+                        void* stream);
+/* Gather-GEMM with packed weights: out[m, n] = bias[n] + sum_k sum_r
+ * A[pairs[k, m], r] * W[k](n, r), A [n_src, R] dtype, pairs [kv, M],
+ * out [M, N] out_dtype; N = K (forward) or C (dgrad), R the other one.
+ * has_bias selects the bias packed with the weight. */
+int sp_conv_gemm_packed(const void* a, int32_t dtype, int64_t n_src, const void* packed,
+                        int64_t K, int64_t kv, int64_t C, int32_t transpose, int32_t has_bias,
+                        const int32_t* pairs, int64_t M, const int32_t* pair_mask,
+                        const int32_t* mask_argsort, void* out, int32_t out_dtype, void* stream);
+
+/* Forward: out[m, n] = bias[n] + sum_k sum_c X[pf[k, m], c] * W[n, k, c].
+ * X [n_in, C] dtype; W [K, kv, C] w_dtype; pf [kv, n_out]; bias [K] of
+ * w_dtype (nullable); out [n_out, K] out_dtype.  pair_mask/mask_argsort [n_out]
+ * (both nullable, kv <= 32) select the masked path: rows are visited in
+ * argsort order and offsets empty across a row tile are skipped (identical
+ * result).  Accumulation is fp32.  Replaces conv_forward + _gather_gemm_kernel,
+ * spconv_triton/pytorch/_impl/gemm.py:206-321, :501-568. */
+int sp_conv_fwd(const void* x, int32_t dtype, int64_t n_in, int64_t C,
+                const void* w, int32_t w_dtype, int64_t K, int64_t kv,
+                const int32_t* pf, int64_t n_out, const void* bias,
+                const int32_t* pair_mask, const int32_t* mask_argsort,
+                void* out, int32_t out_dtype, void* ws, size_t ws_bytes, void* stream);
+
+/* Input gradient: dX[j, c] = sum_k sum_n G[pb[k, j], n] * W[n, k, c].
+ * G [n_out, K]; pb [kv, n_in]; dX [n_in, C] in dtype.
+ * Replaces conv_backward_input, gemm.py:571-631. */
+int sp_conv_dgrad(const void* g, int32_t dtype, int64_t n_out, int64_t K,
+                  const void* w, int32_t w_dtype, int64_t kv, int64_t C,
+                  const int32_t* pb, int64_t n_in,
+                  const int32_t* pair_mask, const int32_t* mask_argsort,
+                  void* dx, void* ws, size_t ws_bytes, void* stream);
+
+/* Weight gradient over compacted pairs (sp_compact_table of pair_fwd):
+ * dW[n, k, c] = sum_{p < counts[k]} X[in_rows[k, p], c] * G[out_rows[k, p], n].
+ * X [n_in, C], G [n_out, K]; in_rows/out_rows [kv, row_stride].  Split-P fp32 partials reduced in a fixed
+ * order (deterministic).  dW [K, kv, C] in dtype.
+ * Replaces conv_backward_weight + _dweight_masked_kernel, gemm.py:324-453, :634-713. */
+size_t sp_wgrad_workspace_size(int64_t K, int64_t kv, int64_t C, int64_t n_rows);
+int sp_conv_wgrad(const void* x, int64_t n_in, const void* g, int64_t n_out, int32_t dtype,
+                  int64_t C, int64_t K, int64_t kv, const int32_t* in_rows,
+                  const int32_t* out_rows, const int32_t* counts, int64_t row_stride,
+                  void* dw, void* ws, size_t ws_bytes, void* stream);
+
+/* ---- pooling (spconv_triton/pytorch/_impl/pool.py) --------------------- */
+
+/* out[m, c] = max(0, max_{k: pf[k,m] >= 0} X[pf[k,m], c]); fp32 accumulator
+ * (fp64 for SP_F64).  Replaces maxpool_forward, pool.py:45-91, :260-284. */
+int sp_maxpool_fwd(const void* x, int32_t dtype, int64_t n_in, int64_t C,
+                   const int32_t* pf, int64_t kv, int64_t n_out, void* out, void* stream);
+
+/* dX[j, c] = sum_{k: pb[k,j] >= 0, out[pb,c] == X[j,c]} G[pb[k,j], c].
+ * Replaces maxpool_backward, pool.py:94-154, :287-330. */
+int sp_maxpool_bwd(const void* x, const void* out, const void* gout, int32_t dtype,
+                   int64_t n_in, int64_t C, const int32_t* pb, int64_t kv, int64_t n_out,
+                   void* dx, void* stream);
+
+/* Mean over present inputs; count [n_out] int32 (nullable).
+ * Replaces avgpool_forward, pool.py:157-208, :333-367. */
+int sp_avgpool_fwd(const void* x, int32_t dtype, int64_t n_in, int64_t C,
+                   const int32_t* pf, int64_t kv, int64_t n_out, void* out,
+                   int32_t* count, void* stream);
+
+/* dX[j, c] = sum_{k: pb[k,j] >= 0} G[pb[k,j], c] * count[pb[k,j]] (the
+ * reference multiplies by the count).  Replaces avgpool_backward,
+ * pool.py:211-257, :370-397. */
+int sp_avgpool_bwd(const void* gout, const int32_t* count, int32_t dtype, int64_t n_out,
+                   int64_t C, const int32_t* pb, int64_t kv, int64_t n_in, void* dx,
+                   void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPCONV_HIP_H */

@@ -1,0 +1,590 @@
+// Implicit gather-GEMM for sparse convolution on gfx950 (CDNA4 MFMA).
+//
+// Forward and input-gradient share one output-stationary kernel
+// (the reference does the same, spconv_triton/pytorch/_impl/gemm.py:206-321):
+//
+//   out[m, n] = bias[n] + sum_k sum_r A[pairs[k, m], r] * B[k][n][r]
+//
+// Work split: a workgroup is 4 waves; each wave owns 64 output rows x 64
+// output columns = 2 x 2 tiles of v_mfma_f32_32x32x16_{f16,bf16} (or
+// v_mfma_f32_32x32x2f32 for fp32).  A rows are gathered straight from global
+// memory into the MFMA A operand: lane l holds row (l % 32) and 16 contiguous
+// bytes of the reduction dimension, so a gather is one 16-byte load per lane.
+// B (the weights) is relaid once per call into [k][r / V][n][V] (V elements
+// = 16 bytes), which makes every B operand load a fully coalesced 1 KiB read.
+// Any assignment of reduction indices to (MFMA step, lane half, element) is
+// valid as long as A and B use the same one; both use r = r0 + half*V + e.
+//
+// Masked mode (MaskImplicitGemm, gemm.py:282-296): rows are visited in
+// mask_argsort order; the OR of the 64 rows' offset bitmasks is taken with
+// a wave reduction and offsets empty for the whole wave tile are skipped.
+// Skipped terms are exactly zero, so the result equals the dense one.
+//
+// Weight gradient (gemm.py:324-426): per offset k, dW[k] = X_k^T G_k over the
+// compacted pairs of that offset.  The pair dimension is the MFMA reduction
+// dimension, so gathered rows are staged in LDS transposed ([channel][pair])
+// and read back as 16-byte MFMA operands.  The pair list of each offset is cut
+// into `splits` contiguous ranges whose fp32 partials are summed in a fixed
+// order by a second kernel (deterministic, no atomics).
+#include "sp_common.h"
+
+namespace sp {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<_Float16> {
+  using frag = half8;
+  static constexpr int V = 8;       // elements per 16-byte lane load
+  static constexpr int KSTEP = 16;  // reduction indices per step (2 halves x V)
+  __device__ static __forceinline__ void mma(const frag& a, const frag& b, floatx16& c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma<__bf16> {
+  using frag = bf16x8;
+  static constexpr int V = 8;
+  static constexpr int KSTEP = 16;
+  __device__ static __forceinline__ void mma(const frag& a, const frag& b, floatx16& c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma<float> {
+  using frag = float4v;
+  static constexpr int V = 4;
+  static constexpr int KSTEP = 8;
+  __device__ static __forceinline__ void mma(const frag& a, const frag& b, floatx16& c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[0], b[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[1], b[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[2], b[2], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[3], b[3], c, 0, 0, 0);
+  }
+};
+
+__device__ __forceinline__ float to_f32(_Float16 v) { return float(v); }
+__device__ __forceinline__ float to_f32(__bf16 v) { return float(v); }
+__device__ __forceinline__ float to_f32(float v) { return v; }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float v);
+template <>
+__device__ __forceinline__ _Float16 from_f32<_Float16>(float v) { return _Float16(v); }
+template <>
+__device__ __forceinline__ __bf16 from_f32<__bf16>(float v) { return __bf16(v); }
+template <>
+__device__ __forceinline__ float from_f32<float>(float v) { return v; }
+
+__device__ __forceinline__ float load_any(const void* p, int dtype, int64_t i) {
+  switch (dtype) {
+    case SP_F16: return float(static_cast<const _Float16*>(p)[i]);
+    case SP_BF16: return float(static_cast<const __bf16*>(p)[i]);
+    case SP_F32: return static_cast<const float*>(p)[i];
+    default: return float(static_cast<const double*>(p)[i]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// weight relayout: KRSC [K][kv][C] -> Bt[k][r/V][n][V] (zero padded in r)
+//   forward: n = output channel (K), r = input channel (C)
+//   dgrad:   n = input channel (C),  r = output channel (K)
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ void relayout_weight(const void* __restrict__ w, int w_dtype, int64_t K, int64_t kv,
+                                int64_t C, int transpose, int N, int R, int Rp,
+                                T* __restrict__ bt) {
+  constexpr int V = Mfma<T>::V;
+  const int64_t total = kv * int64_t(Rp) * N;
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int e = int(i % V);
+  int64_t t = i / V;
+  const int n = int(t % N);
+  t /= N;
+  const int rv = int(t % (Rp / V));
+  const int64_t k = t / (Rp / V);
+  const int r = rv * V + e;
+  float v = 0.f;
+  if (r < R) {
+    const int64_t src = transpose ? (int64_t(r) * kv + k) * C + n : (int64_t(n) * kv + k) * C + r;
+    v = load_any(w, w_dtype, src);
+  }
+  bt[i] = from_f32<T>(v);
+}
+
+__global__ void bias_to_f32(const void* __restrict__ b, int dtype, int n, float* __restrict__ out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = b ? load_any(b, dtype, i) : 0.f;
+}
+
+// ---------------------------------------------------------------------------
+// forward / dgrad gather-GEMM
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::frag load_frag_vec(const T* p) {
+  return *reinterpret_cast<const typename Mfma<T>::frag*>(p);
+}
+
+template <typename T, typename OutT, bool MASK, bool VEC>
+__global__ __launch_bounds__(256) void gather_gemm(
+    const T* __restrict__ A, int64_t n_src, const T* __restrict__ Bt,
+    const int32_t* __restrict__ pairs, const int32_t* __restrict__ pmask,
+    const int32_t* __restrict__ argsort, const float* __restrict__ bias, OutT* __restrict__ out,
+    int64_t M, int N, int R, int Rp, int kv) {
+  using MF = Mfma<T>;
+  using frag = typename MF::frag;
+  constexpr int V = MF::V;
+  constexpr int KSTEP = MF::KSTEP;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int64_t slot0 = (int64_t(blockIdx.x) * 4 + wave) * 64;
+  if (slot0 >= M) return;  // whole wave idle; no workgroup barrier below
+  const int n0 = blockIdx.y * 64;
+
+  int64_t rm[2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int64_t slot = slot0 + mt * 32 + l32;
+    rm[mt] = slot < M ? (MASK ? int64_t(argsort[slot]) : slot) : -1;
+    if (rm[mt] >= M) rm[mt] = -1;
+  }
+  uint32_t tmask = 0xFFFFFFFFu;
+  if (MASK) {
+    const int64_t slot = slot0 + lane;
+    tmask = wave_or(slot < M ? uint32_t(pmask[slot]) : 0u);
+  }
+
+  floatx16 acc[2][2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.f;
+
+  const int64_t bk_stride = int64_t(Rp / V) * N * V;  // elements per offset in Bt
+  for (int k = 0; k < kv; ++k) {
+    if (MASK && !((tmask >> k) & 1u)) continue;
+    int64_t src[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      int32_t j = rm[mt] >= 0 ? pairs[int64_t(k) * M + rm[mt]] : -1;
+      src[mt] = (j >= 0 && j < n_src) ? int64_t(j) : -1;
+    }
+    const T* bbase = Bt + int64_t(k) * bk_stride;
+    for (int r0 = 0; r0 < Rp; r0 += KSTEP) {
+      const int rr = r0 + h * V;
+      frag a[2], b[2];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        if (VEC) {
+          if (src[mt] >= 0 && rr < R) {
+            a[mt] = load_frag_vec<T>(A + src[mt] * R + rr);
+          } else {
+#pragma unroll
+            for (int e = 0; e < V; ++e) a[mt][e] = T(0.f);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < V; ++e)
+            a[mt][e] = (src[mt] >= 0 && rr + e < R) ? A[src[mt] * R + rr + e] : T(0.f);
+        }
+      }
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int col = n0 + nt * 32 + l32;
+        if (col < N) {
+          b[nt] = load_frag_vec<T>(bbase + (int64_t(rr / V) * N + col) * V);
+        } else {
+#pragma unroll
+          for (int e = 0; e < V; ++e) b[nt][e] = T(0.f);
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) MF::mma(a[mt], b[nt], acc[mt][nt]);
+    }
+  }
+
+  // epilogue: lane l holds column l%32 of rows 8*(i/4) + 4*h + (i%4)
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int rloc = (i >> 2) * 8 + h * 4 + (i & 3);
+      const int64_t row = __shfl(rm[mt], rloc, 64);
+      if (row < 0) continue;
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        const int col = n0 + nt * 32 + l32;
+        if (col < N) {
+          float v = acc[mt][nt][i];
+          if (bias) v += bias[col];
+          out[row * N + col] = from_f32<OutT>(v);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// weight gradient
+// ---------------------------------------------------------------------------
+constexpr int kWgP = 64;  // pairs per LDS stage
+
+template <typename T>
+__global__ __launch_bounds__(256) void wgrad_partial(
+    const T* __restrict__ X, int64_t n_in, const T* __restrict__ G, int64_t n_out, int C, int K,
+    int kv, const int32_t* __restrict__ in_rows, const int32_t* __restrict__ out_rows,
+    const int32_t* __restrict__ counts, int64_t stride, int splits, float* __restrict__ part) {
+  using MF = Mfma<T>;
+  using frag = typename MF::frag;
+  constexpr int V = MF::V;
+  constexpr int KSTEP = MF::KSTEP;
+  constexpr int PITCH = kWgP + V;  // row pitch in elements (keeps 16-byte alignment)
+  __shared__ __align__(16) T Xs[64][PITCH];
+  __shared__ __align__(16) T Gs[64][PITCH];
+
+  const int k = blockIdx.x / splits;
+  const int split = blockIdx.x % splits;
+  const int c0 = blockIdx.y * 64, n0 = blockIdx.z * 64;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int ctile = (wave >> 1) * 32, ntile = (wave & 1) * 32;
+
+  const int64_t cnt = counts[k];
+  const int64_t chunk = (cnt + splits - 1) / splits;
+  const int64_t p_lo = split * chunk;
+  const int64_t p_hi = p_lo + chunk < cnt ? p_lo + chunk : cnt;
+
+  floatx16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+
+  constexpr int VPR = 64 / V;  // vectors per 64-channel row
+  for (int64_t p0 = p_lo; p0 < p_hi; p0 += kWgP) {
+    __syncthreads();
+    for (int v = threadIdx.x; v < kWgP * VPR; v += 256) {
+      const int prow = v / VPR, cv = v % VPR;
+      const int64_t p = p0 + prow;
+      int32_t i = -1, o = -1;
+      if (p < p_hi) {
+        i = in_rows[int64_t(k) * stride + p];
+        o = out_rows[int64_t(k) * stride + p];
+        if (i >= n_in) i = -1;
+        if (o >= n_out) o = -1;
+      }
+#pragma unroll
+      for (int e = 0; e < V; ++e) {
+        const int c = c0 + cv * V + e;
+        const int n = n0 + cv * V + e;
+        Xs[cv * V + e][prow] = (i >= 0 && c < C) ? X[int64_t(i) * C + c] : T(0.f);
+        Gs[cv * V + e][prow] = (o >= 0 && n < K) ? G[int64_t(o) * K + n] : T(0.f);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < kWgP; s += KSTEP) {
+      const frag a = *reinterpret_cast<const frag*>(&Xs[ctile + l32][s + h * V]);
+      const frag b = *reinterpret_cast<const frag*>(&Gs[ntile + l32][s + h * V]);
+      MF::mma(a, b, acc);
+    }
+  }
+  // D[c][n]: lane holds column n = l32 of rows c = 8*(i/4) + 4*h + (i%4)
+  const int n = n0 + ntile + l32;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int c = c0 + ctile + (i >> 2) * 8 + h * 4 + (i & 3);
+    if (c < C && n < K) part[((int64_t(split) * K + n) * kv + k) * C + c] = acc[i];
+  }
+}
+
+template <typename T>
+__global__ void wgrad_reduce(const float* __restrict__ part, int splits, int64_t total,
+                             T* __restrict__ dw) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  float s = 0.f;
+  for (int p = 0; p < splits; ++p) s += part[int64_t(p) * total + i];
+  dw[i] = from_f32<T>(s);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+static int elem_size(int dtype) {
+  switch (dtype) {
+    case SP_F16: case SP_BF16: return 2;
+    case SP_F32: return 4;
+    case SP_F64: return 8;
+    default: return 0;
+  }
+}
+
+static int vec_of(int dtype) { return dtype == SP_F32 ? 4 : 8; }
+
+static int64_t padded(int64_t r, int v) { return (r + v - 1) / v * v; }
+
+// Packed weight buffer: Bt [kv][Rp/V][N][V] of the compute dtype, then the
+// bias as N floats at a 256-byte aligned offset.
+struct Packed {
+  int N, R, Rp;
+  size_t bt_bytes, bias_off, total;
+};
+
+static Packed packed_layout(int64_t K, int64_t kv, int64_t C, int dtype, int transpose) {
+  Packed p;
+  p.N = int(transpose ? C : K);
+  p.R = int(transpose ? K : C);
+  p.Rp = int(padded(p.R, vec_of(dtype)));
+  p.bt_bytes = size_t(kv) * size_t(p.Rp) * size_t(p.N) * size_t(elem_size(dtype));
+  p.bias_off = align_up(p.bt_bytes, 256);
+  p.total = p.bias_off + align_up(size_t(p.N) * sizeof(float), 256);
+  return p;
+}
+
+static bool gemm_dtype_ok(int dtype) { return dtype == SP_F16 || dtype == SP_BF16 || dtype == SP_F32; }
+
+static int pack_weight(const void* w, int w_dtype, const void* bias, int64_t K, int64_t kv,
+                       int64_t C, int dtype, int transpose, void* packed, hipStream_t s) {
+  SP_CHECK_ARG(gemm_dtype_ok(dtype), "pack: compute dtype %d not supported (f16/bf16/f32)", dtype);
+  SP_CHECK_ARG(elem_size(w_dtype) > 0, "pack: weight dtype %d not supported", w_dtype);
+  SP_CHECK_ARG(K >= 1 && C >= 1 && kv >= 1 && K < 65536 && C < 65536 && kv < 65536,
+               "pack: bad sizes K=%lld kv=%lld C=%lld", (long long)K, (long long)kv, (long long)C);
+  SP_CHECK_ARG(w && packed, "pack: null pointer");
+  const Packed p = packed_layout(K, kv, C, dtype, transpose);
+  const int64_t tot = kv * int64_t(p.Rp) * p.N;
+  const unsigned rb = unsigned(cdiv(tot, 256));
+  char* base = static_cast<char*>(packed);
+  switch (dtype) {
+    case SP_F16:
+      relayout_weight<_Float16><<<rb, 256, 0, s>>>(w, w_dtype, K, kv, C, transpose, p.N, p.R,
+                                                   p.Rp, reinterpret_cast<_Float16*>(base));
+      break;
+    case SP_BF16:
+      relayout_weight<__bf16><<<rb, 256, 0, s>>>(w, w_dtype, K, kv, C, transpose, p.N, p.R, p.Rp,
+                                                 reinterpret_cast<__bf16*>(base));
+      break;
+    default:
+      relayout_weight<float><<<rb, 256, 0, s>>>(w, w_dtype, K, kv, C, transpose, p.N, p.R, p.Rp,
+                                                reinterpret_cast<float*>(base));
+  }
+  SP_LAUNCHED();
+  bias_to_f32<<<unsigned(cdiv(p.N, 256)), 256, 0, s>>>(bias, w_dtype, p.N,
+                                                      reinterpret_cast<float*>(base + p.bias_off));
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+template <typename T, typename OutT>
+static int launch_gemm_typed(const T* A, int64_t n_src, const T* bt, const int32_t* pairs,
+                             const int32_t* pm, const int32_t* ar, const float* bias, void* out,
+                             int64_t M, int N, int R, int Rp, int kv, bool vec, hipStream_t s) {
+  const int64_t gx = cdiv(M, 256);
+  SP_CHECK_ARG(gx <= kMaxGridX, "gemm: too many rows");
+  const dim3 grid{unsigned(gx), unsigned(cdiv(N, 64)), 1u};
+  OutT* o = static_cast<OutT*>(out);
+  const bool mask = pm && ar;
+  if (mask && vec)
+    gather_gemm<T, OutT, true, true><<<grid, 256, 0, s>>>(A, n_src, bt, pairs, pm, ar, bias, o, M,
+                                                         N, R, Rp, kv);
+  else if (mask)
+    gather_gemm<T, OutT, true, false><<<grid, 256, 0, s>>>(A, n_src, bt, pairs, pm, ar, bias, o, M,
+                                                          N, R, Rp, kv);
+  else if (vec)
+    gather_gemm<T, OutT, false, true><<<grid, 256, 0, s>>>(A, n_src, bt, pairs, pm, ar, bias, o, M,
+                                                          N, R, Rp, kv);
+  else
+    gather_gemm<T, OutT, false, false><<<grid, 256, 0, s>>>(A, n_src, bt, pairs, pm, ar, bias, o,
+                                                           M, N, R, Rp, kv);
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+template <typename T>
+static int launch_gemm_out(int out_dtype, const T* A, int64_t n_src, const T* bt,
+                           const int32_t* pairs, const int32_t* pm, const int32_t* ar,
+                           const float* bias, void* out, int64_t M, int N, int R, int Rp, int kv,
+                           bool vec, hipStream_t s) {
+  switch (out_dtype) {
+    case SP_F16:
+      return launch_gemm_typed<T, _Float16>(A, n_src, bt, pairs, pm, ar, bias, out, M, N, R, Rp,
+                                            kv, vec, s);
+    case SP_BF16:
+      return launch_gemm_typed<T, __bf16>(A, n_src, bt, pairs, pm, ar, bias, out, M, N, R, Rp, kv,
+                                          vec, s);
+    case SP_F32:
+      return launch_gemm_typed<T, float>(A, n_src, bt, pairs, pm, ar, bias, out, M, N, R, Rp, kv,
+                                         vec, s);
+    default:
+      return set_error(SP_ERR_UNSUPPORTED, "gemm: output dtype %d not supported", out_dtype);
+  }
+}
+
+static int gemm_packed(const void* A, int dtype, int64_t n_src, const void* packed, int64_t K,
+                       int64_t kv, int64_t C, int transpose, int has_bias, const int32_t* pairs,
+                       int64_t M, const int32_t* pm, const int32_t* ar, void* out, int out_dtype,
+                       hipStream_t s) {
+  SP_CHECK_ARG(gemm_dtype_ok(dtype), "gemm: feature dtype %d not supported (f16/bf16/f32)", dtype);
+  SP_CHECK_ARG(K >= 1 && C >= 1 && kv >= 1 && M >= 0 && n_src >= 0, "gemm: bad sizes");
+  SP_CHECK_ARG(K < 65536 && C < 65536 && kv < 65536, "gemm: channel/kernel size too large");
+  SP_CHECK_ARG(!((pm == nullptr) ^ (ar == nullptr)), "gemm: pair_mask and argsort go together");
+  SP_CHECK_ARG(!(pm && kv > 32), "gemm: masked path needs kv <= 32");
+  if (M == 0) return SP_OK;
+  SP_CHECK_ARG(A && packed && pairs && out, "gemm: null pointer");
+  const Packed p = packed_layout(K, kv, C, dtype, transpose);
+  const char* base = static_cast<const char*>(packed);
+  const float* bias = has_bias ? reinterpret_cast<const float*>(base + p.bias_off) : nullptr;
+  const int V = vec_of(dtype);
+  const bool vec = (p.R % V == 0) && (reinterpret_cast<uintptr_t>(A) % 16 == 0);
+  switch (dtype) {
+    case SP_F16:
+      return launch_gemm_out<_Float16>(out_dtype, static_cast<const _Float16*>(A), n_src,
+                                       reinterpret_cast<const _Float16*>(base), pairs, pm, ar,
+                                       bias, out, M, p.N, p.R, p.Rp, int(kv), vec, s);
+    case SP_BF16:
+      return launch_gemm_out<__bf16>(out_dtype, static_cast<const __bf16*>(A), n_src,
+                                     reinterpret_cast<const __bf16*>(base), pairs, pm, ar, bias,
+                                     out, M, p.N, p.R, p.Rp, int(kv), vec, s);
+    default:
+      return launch_gemm_out<float>(out_dtype, static_cast<const float*>(A), n_src,
+                                    reinterpret_cast<const float*>(base), pairs, pm, ar, bias, out,
+                                    M, p.N, p.R, p.Rp, int(kv), vec, s);
+  }
+}
+
+// Shared body of forward (transpose = 0) and dgrad (transpose = 1): pack the
+// weight into the workspace, then run the packed GEMM.
+static int gemm_common(const void* A, int dtype, int64_t n_src, const void* w, int w_dtype,
+                       int64_t K, int64_t kv, int64_t C, int transpose, const int32_t* pairs,
+                       int64_t M, const void* bias, const int32_t* pm, const int32_t* ar,
+                       void* out, int out_dtype, void* ws, size_t ws_bytes, hipStream_t s) {
+  SP_CHECK_ARG(gemm_dtype_ok(dtype), "gemm: feature dtype %d not supported (f16/bf16/f32)", dtype);
+  if (M == 0) return SP_OK;
+  const Packed p = packed_layout(K, kv, C, dtype, transpose);
+  if (!ws || ws_bytes < p.total)
+    return set_error(SP_ERR_WORKSPACE, "gemm: workspace %zu < %zu", ws_bytes, p.total);
+  int rc = pack_weight(w, w_dtype, bias, K, kv, C, dtype, transpose, ws, s);
+  if (rc) return rc;
+  return gemm_packed(A, dtype, n_src, ws, K, kv, C, transpose, bias != nullptr, pairs, M, pm, ar,
+                     out, out_dtype, s);
+}
+
+static int wgrad_splits(int64_t kv, int64_t C, int64_t K, int64_t n_rows) {
+  const int64_t tiles = kv * cdiv(C, 64) * cdiv(K, 64);
+  int64_t splits = cdiv(1024, tiles);           // aim for ~4 workgroups per CU on 256 CUs
+  const int64_t by_len = cdiv(n_rows, 1024);    // keep >= ~1k rows of work per split
+  if (splits > by_len) splits = by_len;
+  if (splits > 64) splits = 64;
+  if (splits < 1) splits = 1;
+  return int(splits);
+}
+
+}  // namespace sp
+
+using namespace sp;
+
+extern "C" {
+
+size_t sp_conv_workspace_size(int64_t K, int64_t kv, int64_t C, int32_t dtype) {
+  const Packed a = packed_layout(K, kv, C, dtype, 0);
+  const Packed b = packed_layout(K, kv, C, dtype, 1);
+  return a.total > b.total ? a.total : b.total;
+}
+
+size_t sp_conv_packed_bytes(int64_t K, int64_t kv, int64_t C, int32_t dtype, int32_t transpose) {
+  return packed_layout(K, kv, C, dtype, transpose).total;
+}
+
+int sp_conv_pack_weight(const void* w, int32_t w_dtype, const void* bias, int64_t K, int64_t kv,
+                        int64_t C, int32_t dtype, int32_t transpose, void* packed,
+                        void* stream) {
+  return pack_weight(w, w_dtype, bias, K, kv, C, dtype, transpose, packed, as_stream(stream));
+}
+
+int sp_conv_gemm_packed(const void* a, int32_t dtype, int64_t n_src, const void* packed,
+                        int64_t K, int64_t kv, int64_t C, int32_t transpose, int32_t has_bias,
+                        const int32_t* pairs, int64_t M, const int32_t* pair_mask,
+                        const int32_t* mask_argsort, void* out, int32_t out_dtype, void* stream) {
+  return gemm_packed(a, dtype, n_src, packed, K, kv, C, transpose, has_bias, pairs, M, pair_mask,
+                     mask_argsort, out, out_dtype, as_stream(stream));
+}
+
+int sp_conv_fwd(const void* x, int32_t dtype, int64_t n_in, int64_t C, const void* w,
+                int32_t w_dtype, int64_t K, int64_t kv, const int32_t* pf, int64_t n_out,
+                const void* bias, const int32_t* pair_mask, const int32_t* mask_argsort, void* out,
+                int32_t out_dtype, void* ws, size_t ws_bytes, void* stream) {
+  return gemm_common(x, dtype, n_in, w, w_dtype, K, kv, C, 0, pf, n_out, bias, pair_mask,
+                     mask_argsort, out, out_dtype, ws, ws_bytes, as_stream(stream));
+}
+
+int sp_conv_dgrad(const void* g, int32_t dtype, int64_t n_out, int64_t K, const void* w,
+                  int32_t w_dtype, int64_t kv, int64_t C, const int32_t* pb, int64_t n_in,
+                  const int32_t* pair_mask, const int32_t* mask_argsort, void* dx, void* ws,
+                  size_t ws_bytes, void* stream) {
+  return gemm_common(g, dtype, n_out, w, w_dtype, K, kv, C, 1, pb, n_in, nullptr, pair_mask,
+                     mask_argsort, dx, dtype, ws, ws_bytes, as_stream(stream));
+}
+
+size_t sp_wgrad_workspace_size(int64_t K, int64_t kv, int64_t C, int64_t n_rows) {
+  const int splits = wgrad_splits(kv, C, K, n_rows);
+  return align_up(size_t(splits) * size_t(K * kv * C) * sizeof(float), 256);
+}
+
+int sp_conv_wgrad(const void* x, int64_t n_in, const void* g, int64_t n_out, int32_t dtype,
+                  int64_t C, int64_t K, int64_t kv, const int32_t* in_rows,
+                  const int32_t* out_rows, const int32_t* counts, int64_t row_stride, void* dw,
+                  void* ws, size_t ws_bytes, void* stream) {
+  SP_CHECK_ARG(dtype == SP_F16 || dtype == SP_BF16 || dtype == SP_F32,
+               "wgrad: dtype %d not supported (f16/bf16/f32)", dtype);
+  SP_CHECK_ARG(K >= 1 && C >= 1 && kv >= 1 && row_stride >= 0, "wgrad: bad sizes");
+  SP_CHECK_ARG(K < 65536 && C < 65536 && kv < 65536, "wgrad: channel/kernel size too large");
+  SP_CHECK_ARG(x && g && in_rows && out_rows && counts && dw, "wgrad: null pointer");
+  hipStream_t s = as_stream(stream);
+  const int splits = wgrad_splits(kv, C, K, row_stride);
+  const size_t need = sp_wgrad_workspace_size(K, kv, C, row_stride);
+  if (!ws || ws_bytes < need)
+    return set_error(SP_ERR_WORKSPACE, "wgrad: workspace %zu < %zu", ws_bytes, need);
+  float* part = static_cast<float*>(ws);
+  const int64_t gx = kv * splits;
+  SP_CHECK_ARG(gx <= kMaxGridX, "wgrad: grid too large");
+  dim3 grid(unsigned(gx), unsigned(cdiv(C, 64)), unsigned(cdiv(K, 64)));
+  const int64_t tot = K * kv * C;
+  const unsigned rb = unsigned(cdiv(tot, 256));
+  switch (dtype) {
+    case SP_F16:
+      wgrad_partial<_Float16><<<grid, 256, 0, s>>>(
+          static_cast<const _Float16*>(x), n_in, static_cast<const _Float16*>(g), n_out,
+          int(C), int(K), int(kv), in_rows, out_rows, counts, row_stride, splits, part);
+      SP_LAUNCHED();
+      wgrad_reduce<_Float16><<<rb, 256, 0, s>>>(part, splits, tot, static_cast<_Float16*>(dw));
+      break;
+    case SP_BF16:
+      wgrad_partial<__bf16><<<grid, 256, 0, s>>>(
+          static_cast<const __bf16*>(x), n_in, static_cast<const __bf16*>(g), n_out, int(C),
+          int(K), int(kv), in_rows, out_rows, counts, row_stride, splits, part);
+      SP_LAUNCHED();
+      wgrad_reduce<__bf16><<<rb, 256, 0, s>>>(part, splits, tot, static_cast<__bf16*>(dw));
+      break;
+    default:
+      wgrad_partial<float><<<grid, 256, 0, s>>>(
+          static_cast<const float*>(x), n_in, static_cast<const float*>(g), n_out, int(C),
+          int(K), int(kv), in_rows, out_rows, counts, row_stride, splits, part);
+      SP_LAUNCHED();
+      wgrad_reduce<float><<<rb, 256, 0, s>>>(part, splits, tot, static_cast<float*>(dw));
+  }
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+}  // extern "C"

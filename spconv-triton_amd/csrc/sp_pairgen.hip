@@ -1,0 +1,912 @@
+// Rulebook (pair) generation for submanifold, regular and transposed sparse
+// convolution on gfx950.
+//
+// The reference finds neighbours by sorting the input keys and binary
+// searching every (offset, point) candidate (spconv_triton/pytorch/_impl/
+// pairs.py:196-220, pair_kernels.py:298-482).  Here the coordinates go into an
+// open-addressing hash table instead (32-bit keys packed with their row into
+// one 64-bit slot, or 64-bit keys with a side array of rows), and every output
+// row probes its kv neighbours directly ("output stationary"): each thread owns
+// one row and writes column r of every offset row of the table, so the stores
+// of a wave are contiguous, and the per-row offset bitmask comes out of the
+// same loop in registers.
+//
+// Output order is the reference's, bit for bit:
+//  * subm: output rows are the input rows (pairs.py:400-401);
+//  * regular/transpose: output rows are the unique candidate keys in ascending
+//    batch-major order (torch.unique, pairs.py:206-219) -- a radix sort of the
+//    deduplicated keys restores that order, and the sorted position of each key
+//    is written back into its hash slot as its output row.
+#include "sp_common.h"
+#include "sp_sort.h"
+
+namespace sp {
+
+// ---------------------------------------------------------------------------
+// geometry
+// ---------------------------------------------------------------------------
+struct GeomDev {
+  int ndim;
+  int mode;
+  int kv;
+  int64_t batch;
+  int64_t in_shape[4];
+  int64_t out_shape[4];
+  int32_t ks[4], st[4], pad[4], dil[4];
+};
+
+static int64_t prod_shape(const int64_t* s, int ndim) {
+  int64_t p = 1;
+  for (int d = 0; d < ndim; ++d) p *= s[d];
+  return p;
+}
+
+static int make_geom(const sp_geom* g, GeomDev* out) {
+  SP_CHECK_ARG(g != nullptr, "geometry is null");
+  SP_CHECK_ARG(g->ndim >= 1 && g->ndim <= 4, "ndim %d not in 1..4", g->ndim);
+  SP_CHECK_ARG(g->mode >= SP_PAIR_SUBM && g->mode <= SP_PAIR_TRANSPOSE, "bad mode %d", g->mode);
+  SP_CHECK_ARG(g->batch_size >= 1, "batch_size %lld < 1", (long long)g->batch_size);
+  GeomDev d{};
+  d.ndim = g->ndim;
+  d.mode = g->mode;
+  d.batch = g->batch_size;
+  int64_t kv = 1;
+  for (int i = 0; i < g->ndim; ++i) {
+    SP_CHECK_ARG(g->ksize[i] >= 1, "ksize[%d]=%d < 1", i, g->ksize[i]);
+    SP_CHECK_ARG(g->dilation[i] >= 1, "dilation[%d] < 1", i);
+    SP_CHECK_ARG(g->in_shape[i] >= 1 && g->out_shape[i] >= 1, "shape[%d] must be >= 1", i);
+    d.in_shape[i] = g->in_shape[i];
+    d.out_shape[i] = g->out_shape[i];
+    d.ks[i] = g->ksize[i];
+    d.dil[i] = g->dilation[i];
+    if (g->mode == SP_PAIR_SUBM) {
+      SP_CHECK_ARG(g->ksize[i] % 2 == 1, "subm needs odd kernel sizes");
+      SP_CHECK_ARG(g->out_shape[i] == g->in_shape[i], "subm out_shape must equal in_shape");
+      d.pad[i] = (g->ksize[i] / 2) * g->dilation[i];
+      d.st[i] = 1;
+    } else {
+      SP_CHECK_ARG(g->stride[i] >= 1, "stride[%d] < 1", i);
+      d.pad[i] = g->padding[i];
+      d.st[i] = g->stride[i];
+    }
+    kv *= g->ksize[i];
+  }
+  SP_CHECK_ARG(kv <= 4096, "kernel volume %lld too large", (long long)kv);
+  d.kv = int(kv);
+  *out = d;
+  return SP_OK;
+}
+
+static bool need_key64(const GeomDev& g) {
+  // pairs.py:166-171 -- int32 keys iff batch * volume < 2^31
+  const double lim = 2147483648.0;
+  double vo = double(g.batch);
+  double vi = double(g.batch);
+  for (int d = 0; d < g.ndim; ++d) {
+    vo *= double(g.out_shape[d]);
+    vi *= double(g.in_shape[d]);
+  }
+  if (g.mode == SP_PAIR_SUBM) vo = vo > vi ? vo : vi;
+  return vo >= lim;
+}
+
+static int bit_length_u64(uint64_t v) { return v ? 64 - __builtin_clzll(v) : 0; }
+
+// ---------------------------------------------------------------------------
+// hash tables
+// ---------------------------------------------------------------------------
+constexpr uint64_t kEmpty64 = ~uint64_t(0);
+
+__device__ __forceinline__ uint32_t mix32(uint32_t k) {
+  // lowbias32 integer finaliser (Chris Wellons, public domain)
+  k ^= k >> 16;
+  k *= 0x7feb352du;
+  k ^= k >> 15;
+  k *= 0x846ca68bu;
+  k ^= k >> 16;
+  return k;
+}
+
+__device__ __forceinline__ uint64_t mix64(uint64_t k) {
+  // splitmix64 finaliser (Steele, Lea, Flood 2014)
+  k ^= k >> 30;
+  k *= 0xbf58476d1ce4e5b9ull;
+  k ^= k >> 27;
+  k *= 0x94d049bb133111ebull;
+  k ^= k >> 31;
+  return k;
+}
+
+// 32-bit keys: slot = (row << 32) | key; all-ones is the empty slot (keys are
+// < 2^31, so no key is 0xFFFFFFFF).
+struct Table32 {
+  uint64_t* slots;
+  uint64_t mask;
+  int* overflow;
+
+  __device__ __forceinline__ uint64_t home(uint64_t key) const { return mix32(uint32_t(key)) & mask; }
+
+  // Returns true when this call inserted the key.  An existing key keeps the
+  // smaller row value.
+  __device__ bool insert(uint64_t key64, int32_t val) const {
+    const uint32_t key = uint32_t(key64);
+    const uint64_t desired = (uint64_t(uint32_t(val)) << 32) | key;
+    uint64_t s = home(key64);
+    for (uint64_t i = 0; i <= mask; ++i) {
+      const uint64_t prev = atomicCAS((unsigned long long*)&slots[s], (unsigned long long)kEmpty64,
+                                      (unsigned long long)desired);
+      if (prev == kEmpty64) return true;
+      if (uint32_t(prev) == key) {
+        atomicMin(reinterpret_cast<int32_t*>(&slots[s]) + 1, val);
+        return false;
+      }
+      s = (s + 1) & mask;
+    }
+    atomicExch(overflow, 1);
+    return false;
+  }
+
+  __device__ __forceinline__ int64_t find_slot(uint64_t key64) const {
+    const uint32_t key = uint32_t(key64);
+    uint64_t s = home(key64);
+    for (uint64_t i = 0; i <= mask; ++i) {
+      const uint64_t v = slots[s];
+      if (uint32_t(v) == key) return int64_t(s);
+      if (v == kEmpty64) return -1;
+      s = (s + 1) & mask;
+    }
+    return -1;
+  }
+
+  __device__ __forceinline__ int32_t find(uint64_t key64) const {
+    const uint32_t key = uint32_t(key64);
+    uint64_t s = home(key64);
+    for (uint64_t i = 0; i <= mask; ++i) {
+      const uint64_t v = slots[s];
+      if (uint32_t(v) == key) return int32_t(uint32_t(v >> 32));
+      if (v == kEmpty64) return -1;
+      s = (s + 1) & mask;
+    }
+    return -1;
+  }
+
+  __device__ __forceinline__ void set_value(int64_t slot, int32_t val) const {
+    reinterpret_cast<int32_t*>(&slots[slot])[1] = val;
+  }
+};
+
+// 64-bit keys (key volume >= 2^31): key array + row array.
+struct Table64 {
+  uint64_t* keys;
+  int32_t* vals;
+  uint64_t mask;
+  int* overflow;
+
+  __device__ __forceinline__ uint64_t home(uint64_t key) const { return mix64(key) & mask; }
+
+  __device__ bool insert(uint64_t key, int32_t val) const {
+    uint64_t s = home(key);
+    for (uint64_t i = 0; i <= mask; ++i) {
+      const uint64_t prev = atomicCAS((unsigned long long*)&keys[s], (unsigned long long)kEmpty64,
+                                      (unsigned long long)key);
+      if (prev == kEmpty64 || prev == key) {
+        atomicMin(&vals[s], val);
+        return prev == kEmpty64;
+      }
+      s = (s + 1) & mask;
+    }
+    atomicExch(overflow, 1);
+    return false;
+  }
+
+  __device__ __forceinline__ int64_t find_slot(uint64_t key) const {
+    uint64_t s = home(key);
+    for (uint64_t i = 0; i <= mask; ++i) {
+      const uint64_t v = keys[s];
+      if (v == key) return int64_t(s);
+      if (v == kEmpty64) return -1;
+      s = (s + 1) & mask;
+    }
+    return -1;
+  }
+
+  __device__ __forceinline__ int32_t find(uint64_t key) const {
+    const int64_t s = find_slot(key);
+    return s >= 0 ? vals[s] : -1;
+  }
+
+  __device__ __forceinline__ void set_value(int64_t slot, int32_t val) const { vals[slot] = val; }
+};
+
+__global__ void fill_u64(uint64_t* __restrict__ p, int64_t n, uint64_t v) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+__global__ void fill_i32(int32_t* __restrict__ p, int64_t n, int32_t v) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+static int launch_fill_i32(int32_t* p, int64_t n, int32_t v, hipStream_t s) {
+  if (n <= 0) return SP_OK;
+  const int64_t blocks = cdiv(n, 256);
+  SP_CHECK_ARG(blocks <= kMaxGridX, "fill: too many elements");
+  fill_i32<<<dim3(unsigned(blocks)), dim3(256), 0, s>>>(p, n, v);
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+static int launch_fill_u64(uint64_t* p, int64_t n, uint64_t v, hipStream_t s) {
+  if (n <= 0) return SP_OK;
+  const int64_t blocks = cdiv(n, 256);
+  SP_CHECK_ARG(blocks <= kMaxGridX, "fill: too many elements");
+  fill_u64<<<dim3(unsigned(blocks)), dim3(256), 0, s>>>(p, n, v);
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// coordinate helpers
+// ---------------------------------------------------------------------------
+struct Coord {
+  int64_t b;
+  int64_t x[4];
+  bool ok;  // batch and coordinates inside [0, batch) x [0, shape)
+};
+
+__device__ __forceinline__ Coord load_coord(const int32_t* __restrict__ idx, int64_t row,
+                                            const GeomDev& g) {
+  Coord c;
+  const int32_t* p = idx + row * (g.ndim + 1);
+  c.b = p[0];
+  c.ok = c.b >= 0 && c.b < g.batch;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    if (d < g.ndim) {
+      c.x[d] = p[d + 1];
+      c.ok = c.ok && c.x[d] >= 0 && c.x[d] < g.in_shape[d];
+    }
+  }
+  return c;
+}
+
+// Candidate output key for (offset odometer `off`, input coordinate c)
+// following pair_kernels.py:76-91; returns false when geometrically invalid.
+__device__ __forceinline__ bool candidate_key(const GeomDev& g, const Coord& c, const int* off,
+                                              uint64_t* key) {
+  int64_t acc = c.b;
+  bool ok = c.ok;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    if (d < g.ndim) {
+      const int64_t koff = int64_t(off[d]) * g.dil[d];
+      int64_t o;
+      if (g.mode == SP_PAIR_TRANSPOSE) {
+        o = c.x[d] * g.st[d] - g.pad[d] + koff;
+      } else {
+        const int64_t num = c.x[d] + g.pad[d] - koff;
+        if (g.st[d] == 1) {
+          o = num;
+        } else {
+          ok = ok && num >= 0 && (num % g.st[d]) == 0;
+          o = num >= 0 ? num / g.st[d] : -1;
+        }
+      }
+      ok = ok && o >= 0 && o < g.out_shape[d];
+      acc = acc * g.out_shape[d] + o;
+    }
+  }
+  *key = uint64_t(acc);
+  return ok;
+}
+
+// Input key of the k-th neighbour feeding output coordinate c (subm):
+// x_in = x_out - pad + off*dil (the inverse of the subm candidate formula).
+__device__ __forceinline__ bool subm_source_key(const GeomDev& g, const Coord& c, const int* off,
+                                                uint64_t* key) {
+  int64_t acc = c.b;
+  bool ok = c.ok;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    if (d < g.ndim) {
+      const int64_t q = c.x[d] - g.pad[d] + int64_t(off[d]) * g.dil[d];
+      ok = ok && q >= 0 && q < g.in_shape[d];
+      acc = acc * g.in_shape[d] + q;
+    }
+  }
+  *key = uint64_t(acc);
+  return ok;
+}
+
+__device__ __forceinline__ void odometer_next(const GeomDev& g, int* off) {
+  for (int d = g.ndim - 1; d >= 0; --d) {
+    if (++off[d] < g.ks[d]) return;
+    off[d] = 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// subm
+// ---------------------------------------------------------------------------
+template <class Table>
+__global__ __launch_bounds__(256) void subm_insert(const int32_t* __restrict__ idx, int64_t n,
+                                                   GeomDev g, Table t) {
+  const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  Coord c = load_coord(idx, r, g);
+  if (!c.ok) return;
+  int64_t acc = c.b;
+  for (int d = 0; d < g.ndim; ++d) acc = acc * g.in_shape[d] + c.x[d];
+  t.insert(uint64_t(acc), int32_t(r));
+}
+
+// One thread per output row r.  pf[k, r] = row of neighbour k, or -1;
+// pb[kv-1-k, r] = the same value (for odd kernels the subm relation is
+// symmetric: x_r + pad - off_k*dil == x_r - pad + off_{kv-1-k}*dil).
+template <class Table>
+__global__ __launch_bounds__(256) void subm_probe(const int32_t* __restrict__ idx, int64_t n,
+                                                  GeomDev g, Table t, int32_t* __restrict__ pf,
+                                                  int32_t* __restrict__ pb,
+                                                  uint32_t* __restrict__ words, int mic) {
+  const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const Coord c = load_coord(idx, r, g);
+  int off[4] = {0, 0, 0, 0};
+  uint32_t word = 0;
+  for (int k = 0; k < g.kv; ++k) {
+    uint64_t key;
+    int32_t j = -1;
+    if (subm_source_key(g, c, off, &key)) j = t.find(key);
+    if (pf) pf[int64_t(k) * n + r] = j;
+    if (pb) pb[int64_t(g.kv - 1 - k) * n + r] = j;
+    if (j >= 0) word |= 1u << (k & 31);
+    if ((k & 31) == 31 || k == g.kv - 1) {
+      if (words) words[r * mic + (k >> 5)] = word;
+      word = 0;
+    }
+    odometer_next(g, off);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// regular / transpose
+// ---------------------------------------------------------------------------
+struct ConvWs {
+  int* flags;          // [0] overflow
+  uint32_t* counter;   // number of unique keys
+  void* table_a;       // Table32 slots or Table64 keys
+  int32_t* table_vals; // Table64 rows
+  void* list;          // unique keys (u32 or u64)
+  void* tmp;           // radix-sort ping-pong buffer
+  void* sort_ws;
+  uint64_t cap;
+  int64_t bound;
+};
+
+static int64_t conv_bound(const GeomDev& g, int64_t n) {
+  // unique outputs <= min(kv * n, batch * prod(out_shape))
+  double a = double(g.kv) * double(n);
+  double b = double(g.batch) * double(prod_shape(g.out_shape, g.ndim));
+  double m = a < b ? a : b;
+  return int64_t(m < 1.0 ? 1.0 : m);
+}
+
+static uint64_t table_capacity(int64_t items) {
+  uint64_t want = uint64_t(items) * 2;
+  uint64_t cap = 1024;
+  while (cap < want) cap <<= 1;
+  return cap;
+}
+
+template <class W>
+static void conv_layout(W& w, const GeomDev& g, int64_t n, bool key64, ConvWs* out) {
+  const int64_t bound = conv_bound(g, n);
+  const uint64_t cap = table_capacity(bound);
+  auto* flags = w.template take<int>(64);
+  auto* counter = w.template take<uint32_t>(64);
+  void* ta = w.template take<uint64_t>(cap);
+  int32_t* tv = key64 ? w.template take<int32_t>(cap) : nullptr;
+  void* list = key64 ? (void*)w.template take<uint64_t>(size_t(bound))
+                     : (void*)w.template take<uint32_t>(size_t(bound));
+  void* tmp = key64 ? (void*)w.template take<uint64_t>(size_t(bound))
+                    : (void*)w.template take<uint32_t>(size_t(bound));
+  void* sws = w.template take<char>(sort_keys_ws_bytes(bound));
+  if (out) {
+    out->flags = flags;
+    out->counter = counter;
+    out->table_a = ta;
+    out->table_vals = tv;
+    out->list = list;
+    out->tmp = tmp;
+    out->sort_ws = sws;
+    out->cap = cap;
+    out->bound = bound;
+  }
+}
+
+// Sizer variant returning nulls (the WsSizer::take returns void).
+struct WsSizerP {
+  size_t off = 0;
+  template <typename T>
+  T* take(size_t count) {
+    off = align_up(off, 256);
+    off += count * sizeof(T);
+    return nullptr;
+  }
+};
+
+template <class W>
+static void subm_layout(W& w, int64_t n, bool key64, void** ta, int32_t** tv, int** flags,
+                        uint64_t* cap_out) {
+  const uint64_t cap = table_capacity(n);
+  *flags = w.template take<int>(64);
+  *ta = w.template take<uint64_t>(cap);
+  *tv = key64 ? w.template take<int32_t>(cap) : nullptr;
+  *cap_out = cap;
+}
+
+template <class Table, typename KeyT>
+__global__ __launch_bounds__(256) void conv_insert(const int32_t* __restrict__ idx, int64_t n,
+                                                   GeomDev g, Table t, KeyT* __restrict__ list,
+                                                   uint32_t* __restrict__ counter, int64_t bound) {
+  const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const bool live = j < n;
+  Coord c;
+  if (live) c = load_coord(idx, j, g);
+  else c.ok = false;
+  int off[4] = {0, 0, 0, 0};
+  for (int k = 0; k < g.kv; ++k) {
+    uint64_t key = 0;
+    bool fresh = false;
+    if (live && candidate_key(g, c, off, &key)) fresh = t.insert(key, 0);
+    // wave-aggregated append of newly inserted keys
+    const uint64_t b = __ballot(fresh);
+    if (b) {
+      const int leader = __ffsll((unsigned long long)b) - 1;
+      uint32_t base = 0;
+      if (lane_id() == leader) base = atomicAdd(counter, uint32_t(__popcll(b)));
+      base = __shfl(base, leader, 64);
+      if (fresh) {
+        const int64_t pos = int64_t(base) + __popcll(b & lanemask_lt());
+        if (pos < bound) list[pos] = KeyT(key);
+      }
+    }
+    odometer_next(g, off);
+  }
+}
+
+template <class Table, typename KeyT>
+__global__ void conv_rank(const KeyT* __restrict__ sorted, int64_t n_out, Table t) {
+  const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n_out) return;
+  const int64_t s = t.find_slot(uint64_t(sorted[r]));
+  if (s >= 0) t.set_value(s, int32_t(r));
+}
+
+template <typename KeyT>
+__global__ void copy_keys(const KeyT* __restrict__ src, KeyT* __restrict__ dst, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = src[i];
+}
+
+template <typename KeyT>
+__global__ void delinearize(const KeyT* __restrict__ keys, int64_t n, GeomDev g,
+                            int32_t* __restrict__ out) {
+  const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  uint64_t rem = uint64_t(keys[r]);
+  int32_t* o = out + r * (g.ndim + 1);
+  for (int d = g.ndim - 1; d >= 0; --d) {
+    const uint64_t s = uint64_t(g.out_shape[d]);
+    o[d + 1] = int32_t(rem % s);
+    rem /= s;
+  }
+  o[0] = int32_t(rem);
+}
+
+// One thread per input row j: pb[k, j] = output row of candidate (k, j) or -1,
+// pf[k, pb[k, j]] = j; the backward bitmask of row j is built in registers.
+template <class Table>
+__global__ __launch_bounds__(256) void conv_fill(const int32_t* __restrict__ idx, int64_t n,
+                                                 GeomDev g, Table t, int64_t n_keep,
+                                                 int32_t* __restrict__ pf, int32_t* __restrict__ pb,
+                                                 uint32_t* __restrict__ words, int mic) {
+  const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  const Coord c = load_coord(idx, j, g);
+  int off[4] = {0, 0, 0, 0};
+  uint32_t word = 0;
+  for (int k = 0; k < g.kv; ++k) {
+    uint64_t key;
+    int32_t r = -1;
+    if (candidate_key(g, c, off, &key)) {
+      r = t.find(key);
+      if (r >= n_keep) r = -1;
+    }
+    if (r >= 0) {
+      if (pf) pf[int64_t(k) * n_keep + r] = int32_t(j);
+      word |= 1u << (k & 31);
+    }
+    if (pb) pb[int64_t(k) * n + j] = r;
+    if ((k & 31) == 31 || k == g.kv - 1) {
+      if (words) words[j * mic + (k >> 5)] = word;
+      word = 0;
+    }
+    odometer_next(g, off);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// mask words, compaction, native -> tables
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mask_words_kernel(const int32_t* __restrict__ table,
+                                                         int64_t kv, int64_t n,
+                                                         uint32_t* __restrict__ words, int mic) {
+  const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  uint32_t word = 0;
+  for (int64_t k = 0; k < kv; ++k) {
+    if (table[k * n + r] >= 0) word |= 1u << (k & 31);
+    if ((k & 31) == 31 || k == kv - 1) {
+      words[r * mic + (k >> 5)] = word;
+      word = 0;
+    }
+  }
+}
+
+constexpr int kCompactThreads = 256;
+constexpr int kCompactRounds = 8;
+constexpr int kCompactTile = kCompactThreads * kCompactRounds;
+
+// grid (tiles, kv): number of valid entries per (row k, tile)
+__global__ __launch_bounds__(kCompactThreads) void compact_count(const int32_t* __restrict__ table,
+                                                                 int64_t n, int64_t ntiles,
+                                                                 uint32_t* __restrict__ cnt) {
+  __shared__ uint32_t lds[kCompactThreads / 64 + 1];
+  const int64_t k = blockIdx.y;
+  const int64_t base = int64_t(blockIdx.x) * kCompactTile;
+  uint32_t s = 0;
+#pragma unroll
+  for (int r = 0; r < kCompactRounds; ++r) {
+    const int64_t i = base + r * kCompactThreads + threadIdx.x;
+    if (i < n && table[k * n + i] >= 0) ++s;
+  }
+  uint32_t tot;
+  block_exclusive_scan<kCompactThreads>(s, lds, &tot);
+  if (threadIdx.x == 0) cnt[k * ntiles + blockIdx.x] = tot;
+}
+
+__global__ __launch_bounds__(kCompactThreads) void compact_scatter(
+    const int32_t* __restrict__ table, int64_t n, int64_t ntiles, const uint32_t* __restrict__ off,
+    int32_t* __restrict__ pos_out, int32_t* __restrict__ val_out) {
+  __shared__ uint32_t lds[kCompactThreads / 64 + 1];
+  const int64_t k = blockIdx.y;
+  const int64_t base = int64_t(blockIdx.x) * kCompactTile;
+  // segmented: subtract the start of row k in the flat scan
+  uint32_t run = off[k * ntiles + blockIdx.x] - off[k * ntiles];
+  for (int r = 0; r < kCompactRounds; ++r) {
+    const int64_t i = base + r * kCompactThreads + threadIdx.x;
+    int32_t v = -1;
+    if (i < n) v = table[k * n + i];
+    const uint32_t flag = v >= 0 ? 1u : 0u;
+    uint32_t tot;
+    const uint32_t pre = block_exclusive_scan<kCompactThreads>(flag, lds, &tot);
+    if (flag) {
+      const int64_t p = k * n + run + pre;
+      pos_out[p] = int32_t(i);
+      val_out[p] = v;
+    }
+    run += tot;
+  }
+}
+
+__global__ void compact_counts(const uint32_t* __restrict__ off, const uint32_t* __restrict__ total,
+                               int64_t kv, int64_t ntiles, int32_t* __restrict__ counts,
+                               int32_t* __restrict__ npl, int npl_limit) {
+  const int64_t k = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (k >= kv) return;
+  const uint32_t end = (k + 1 < kv) ? off[(k + 1) * ntiles] : *total;
+  const int32_t c = int32_t(end - off[k * ntiles]);
+  if (counts) counts[k] = c;
+  if (npl) npl[k] = k < npl_limit ? c : 0;
+}
+
+__global__ void native_scatter(const int32_t* __restrict__ pin, const int32_t* __restrict__ pout,
+                               int64_t kv, int64_t np, int64_t n_in, int64_t n_out,
+                               int32_t* __restrict__ pf, int32_t* __restrict__ pb) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= kv * np) return;
+  const int64_t k = i / np;
+  const int32_t a = pin[i], b = pout[i];
+  if (a >= 0 && b >= 0 && a < n_in && b < n_out) {
+    pf[k * n_out + b] = a;
+    if (pb) pb[k * n_in + a] = b;
+  }
+}
+
+}  // namespace sp
+
+using namespace sp;
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int sp_geom_key64(const sp_geom* g) {
+  GeomDev d;
+  if (make_geom(g, &d)) return -1;
+  return need_key64(d) ? 1 : 0;
+}
+
+size_t sp_pairgen_workspace_size(const sp_geom* g, int64_t n) {
+  GeomDev d;
+  if (make_geom(g, &d)) return 0;
+  if (n < 1) n = 1;
+  const bool key64 = need_key64(d);
+  if (d.mode == SP_PAIR_SUBM) {
+    WsSizerP z;
+    void* ta;
+    int32_t* tv;
+    int* fl;
+    uint64_t cap;
+    subm_layout(z, n, key64, &ta, &tv, &fl, &cap);
+    return z.off;
+  }
+  WsSizerP z;
+  conv_layout(z, d, n, key64, nullptr);
+  return z.off;
+}
+
+int sp_pairgen_subm(const sp_geom* g, const int32_t* indices, int64_t n, int32_t* pair_fwd,
+                    int32_t* pair_bwd, uint32_t* mask_words, void* ws, size_t ws_bytes,
+                    void* stream) {
+  GeomDev d;
+  int rc = make_geom(g, &d);
+  if (rc) return rc;
+  SP_CHECK_ARG(d.mode == SP_PAIR_SUBM, "sp_pairgen_subm needs SP_PAIR_SUBM");
+  SP_CHECK_ARG(n >= 1 && n < (int64_t(1) << 31), "n=%lld out of range", (long long)n);
+  SP_CHECK_ARG(indices && (pair_fwd || pair_bwd), "null pointer");
+  const size_t need = sp_pairgen_workspace_size(g, n);
+  if (!ws || ws_bytes < need)
+    return set_error(SP_ERR_WORKSPACE, "pairgen_subm: workspace %zu < %zu", ws_bytes, need);
+  hipStream_t s = as_stream(stream);
+  const bool key64 = need_key64(d);
+  WsCursor c(ws, ws_bytes);
+  void* ta;
+  int32_t* tv;
+  int* flags;
+  uint64_t cap;
+  subm_layout(c, n, key64, &ta, &tv, &flags, &cap);
+  const int mic = (d.kv + 31) / 32;
+  const unsigned blocks = unsigned(cdiv(n, 256));
+  rc = launch_fill_u64(static_cast<uint64_t*>(ta), int64_t(cap), kEmpty64, s);
+  if (rc) return rc;
+  if (key64) {
+    rc = launch_fill_i32(tv, int64_t(cap), 0x7fffffff, s);
+    if (rc) return rc;
+    Table64 t{static_cast<uint64_t*>(ta), tv, cap - 1, flags};
+    subm_insert<<<blocks, 256, 0, s>>>(indices, n, d, t);
+    SP_LAUNCHED();
+    subm_probe<<<blocks, 256, 0, s>>>(indices, n, d, t, pair_fwd, pair_bwd, mask_words, mic);
+    SP_LAUNCHED();
+  } else {
+    Table32 t{static_cast<uint64_t*>(ta), cap - 1, flags};
+    subm_insert<<<blocks, 256, 0, s>>>(indices, n, d, t);
+    SP_LAUNCHED();
+    subm_probe<<<blocks, 256, 0, s>>>(indices, n, d, t, pair_fwd, pair_bwd, mask_words, mic);
+    SP_LAUNCHED();
+  }
+  return SP_OK;
+}
+
+int sp_pairgen_conv_build(const sp_geom* g, const int32_t* indices, int64_t n, void* ws,
+                          size_t ws_bytes, int64_t* n_out, void* stream) {
+  GeomDev d;
+  int rc = make_geom(g, &d);
+  if (rc) return rc;
+  SP_CHECK_ARG(d.mode != SP_PAIR_SUBM, "sp_pairgen_conv_build is for regular/transpose convs");
+  SP_CHECK_ARG(n >= 1 && n < (int64_t(1) << 31), "n=%lld out of range", (long long)n);
+  SP_CHECK_ARG(indices && n_out, "null pointer");
+  const size_t need = sp_pairgen_workspace_size(g, n);
+  if (!ws || ws_bytes < need)
+    return set_error(SP_ERR_WORKSPACE, "pairgen_conv_build: workspace %zu < %zu", ws_bytes, need);
+  hipStream_t s = as_stream(stream);
+  const bool key64 = need_key64(d);
+  WsCursor c(ws, ws_bytes);
+  ConvWs w;
+  conv_layout(c, d, n, key64, &w);
+  SP_HIP(hipMemsetAsync(w.flags, 0, 256, s));
+  SP_HIP(hipMemsetAsync(w.counter, 0, 256, s));
+  rc = launch_fill_u64(static_cast<uint64_t*>(w.table_a), int64_t(w.cap), kEmpty64, s);
+  if (rc) return rc;
+  const unsigned blocks = unsigned(cdiv(n, 256));
+  if (key64) {
+    rc = launch_fill_i32(w.table_vals, int64_t(w.cap), 0x7fffffff, s);
+    if (rc) return rc;
+    Table64 t{static_cast<uint64_t*>(w.table_a), w.table_vals, w.cap - 1, w.flags};
+    conv_insert<Table64, uint64_t><<<blocks, 256, 0, s>>>(
+        indices, n, d, t, static_cast<uint64_t*>(w.list), w.counter, w.bound);
+  } else {
+    Table32 t{static_cast<uint64_t*>(w.table_a), w.cap - 1, w.flags};
+    conv_insert<Table32, uint32_t><<<blocks, 256, 0, s>>>(
+        indices, n, d, t, static_cast<uint32_t*>(w.list), w.counter, w.bound);
+  }
+  SP_LAUNCHED();
+  uint32_t host[2] = {0, 0};
+  SP_HIP(hipMemcpyAsync(&host[0], w.counter, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  SP_HIP(hipMemcpyAsync(&host[1], w.flags, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  SP_HIP(hipStreamSynchronize(s));
+  if (host[1]) return set_error(SP_ERR_HASH_FULL, "pairgen: coordinate hash overflow");
+  const int64_t cnt = int64_t(host[0]);
+  if (cnt > w.bound) return set_error(SP_ERR_HASH_FULL, "pairgen: %lld keys > bound %lld",
+                                      (long long)cnt, (long long)w.bound);
+  *n_out = cnt;
+  if (cnt == 0) return SP_OK;
+  // sort the unique keys (bits of the largest possible key) and rank them
+  const double vol = double(d.batch) * double(prod_shape(d.out_shape, d.ndim));
+  const int bits = bit_length_u64(uint64_t(vol) - 1);
+  const unsigned rb = unsigned(cdiv(cnt, 256));
+  if (key64) {
+    uint64_t* res = nullptr;
+    rc = sort_keys_u64(static_cast<uint64_t*>(w.list), static_cast<uint64_t*>(w.tmp), cnt, bits,
+                       &res, w.sort_ws, s);
+    if (rc) return rc;
+    if (res != w.list) {
+      copy_keys<<<rb, 256, 0, s>>>(res, static_cast<uint64_t*>(w.list), cnt);
+      SP_LAUNCHED();
+    }
+    Table64 t{static_cast<uint64_t*>(w.table_a), w.table_vals, w.cap - 1, w.flags};
+    conv_rank<<<rb, 256, 0, s>>>(static_cast<const uint64_t*>(w.list), cnt, t);
+  } else {
+    uint32_t* res = nullptr;
+    rc = sort_keys_u32(static_cast<uint32_t*>(w.list), static_cast<uint32_t*>(w.tmp), cnt, bits,
+                       &res, w.sort_ws, s);
+    if (rc) return rc;
+    if (res != w.list) {
+      copy_keys<<<rb, 256, 0, s>>>(res, static_cast<uint32_t*>(w.list), cnt);
+      SP_LAUNCHED();
+    }
+    Table32 t{static_cast<uint64_t*>(w.table_a), w.cap - 1, w.flags};
+    conv_rank<<<rb, 256, 0, s>>>(static_cast<const uint32_t*>(w.list), cnt, t);
+  }
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+int sp_pairgen_conv_fill(const sp_geom* g, const int32_t* indices, int64_t n, const void* ws,
+                         size_t ws_bytes, int64_t n_keep, int32_t* out_indices, int32_t* pair_fwd,
+                         int32_t* pair_bwd, uint32_t* mask_words_bwd, void* stream) {
+  GeomDev d;
+  int rc = make_geom(g, &d);
+  if (rc) return rc;
+  SP_CHECK_ARG(d.mode != SP_PAIR_SUBM, "sp_pairgen_conv_fill is for regular/transpose convs");
+  SP_CHECK_ARG(n >= 1 && n < (int64_t(1) << 31), "n=%lld out of range", (long long)n);
+  SP_CHECK_ARG(indices && out_indices && (pair_fwd || pair_bwd), "null pointer");
+  SP_CHECK_ARG(n_keep >= 1 && n_keep < (int64_t(1) << 31), "n_keep=%lld out of range",
+               (long long)n_keep);
+  const size_t need = sp_pairgen_workspace_size(g, n);
+  if (!ws || ws_bytes < need)
+    return set_error(SP_ERR_WORKSPACE, "pairgen_conv_fill: workspace %zu < %zu", ws_bytes, need);
+  SP_CHECK_ARG(n_keep <= conv_bound(d, n), "n_keep exceeds the number of candidate outputs");
+  hipStream_t s = as_stream(stream);
+  const bool key64 = need_key64(d);
+  WsCursor c(const_cast<void*>(ws), ws_bytes);
+  ConvWs w;
+  conv_layout(c, d, n, key64, &w);
+  const int mic = (d.kv + 31) / 32;
+  if (pair_fwd) {
+    rc = launch_fill_i32(pair_fwd, int64_t(d.kv) * n_keep, -1, s);
+    if (rc) return rc;
+  }
+  const unsigned blocks = unsigned(cdiv(n, 256));
+  const unsigned rb = unsigned(cdiv(n_keep, 256));
+  if (key64) {
+    Table64 t{static_cast<uint64_t*>(w.table_a), w.table_vals, w.cap - 1, w.flags};
+    conv_fill<<<blocks, 256, 0, s>>>(indices, n, d, t, n_keep, pair_fwd, pair_bwd, mask_words_bwd,
+                                     mic);
+    SP_LAUNCHED();
+    delinearize<<<rb, 256, 0, s>>>(static_cast<const uint64_t*>(w.list), n_keep, d, out_indices);
+  } else {
+    Table32 t{static_cast<uint64_t*>(w.table_a), w.cap - 1, w.flags};
+    conv_fill<<<blocks, 256, 0, s>>>(indices, n, d, t, n_keep, pair_fwd, pair_bwd, mask_words_bwd,
+                                     mic);
+    SP_LAUNCHED();
+    delinearize<<<rb, 256, 0, s>>>(static_cast<const uint32_t*>(w.list), n_keep, d, out_indices);
+  }
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+int sp_mask_words(const int32_t* table, int64_t kv, int64_t n, uint32_t* words, void* stream) {
+  SP_CHECK_ARG(kv >= 1 && n >= 0, "mask_words: bad sizes");
+  if (n == 0) return SP_OK;
+  SP_CHECK_ARG(table && words, "mask_words: null pointer");
+  const int mic = int((kv + 31) / 32);
+  const int64_t blocks = cdiv(n, 256);
+  SP_CHECK_ARG(blocks <= kMaxGridX, "mask_words: n too large");
+  mask_words_kernel<<<unsigned(blocks), 256, 0, as_stream(stream)>>>(table, kv, n, words, mic);
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+static void compact_layout_sizes(int64_t kv, int64_t n, size_t* cnt_words, size_t* total) {
+  const int64_t ntiles = cdiv(n > 0 ? n : 1, kCompactTile);
+  *cnt_words = size_t(kv * ntiles);
+  WsSizer z;
+  z.take<uint32_t>(*cnt_words);
+  z.take<uint32_t>(64);
+  z.take<char>(scan_workspace_bytes(int64_t(*cnt_words)));
+  *total = z.off;
+}
+
+size_t sp_compact_workspace_size(int64_t kv, int64_t n) {
+  size_t cw, tot;
+  compact_layout_sizes(kv, n, &cw, &tot);
+  return tot;
+}
+
+int sp_compact_table(const int32_t* table, int64_t kv, int64_t n, int32_t* pos_out,
+                     int32_t* val_out, int32_t* counts, int32_t* npl, int32_t npl_limit, void* ws,
+                     size_t ws_bytes, void* stream) {
+  SP_CHECK_ARG(kv >= 1 && kv <= 65535 && n >= 0 && n < (int64_t(1) << 31),
+               "compact: bad sizes kv=%lld n=%lld", (long long)kv, (long long)n);
+  SP_CHECK_ARG(table && pos_out && val_out, "compact: null pointer");
+  hipStream_t s = as_stream(stream);
+  size_t cw, need;
+  compact_layout_sizes(kv, n, &cw, &need);
+  if (!ws || ws_bytes < need)
+    return set_error(SP_ERR_WORKSPACE, "compact: workspace %zu < %zu", ws_bytes, need);
+  int rc = launch_fill_i32(pos_out, kv * n, -1, s);
+  if (rc) return rc;
+  rc = launch_fill_i32(val_out, kv * n, -1, s);
+  if (rc) return rc;
+  if (n == 0) {
+    if (counts) { rc = launch_fill_i32(counts, kv, 0, s); if (rc) return rc; }
+    if (npl) { rc = launch_fill_i32(npl, kv, 0, s); if (rc) return rc; }
+    return SP_OK;
+  }
+  WsCursor c(ws, ws_bytes);
+  uint32_t* cnt = c.take<uint32_t>(cw);
+  uint32_t* total = c.take<uint32_t>(64);
+  void* scan_ws = c.take<char>(scan_workspace_bytes(int64_t(cw)));
+  const int64_t ntiles = cdiv(n, kCompactTile);
+  SP_CHECK_ARG(ntiles <= kMaxGridX, "compact: n too large");
+  const dim3 grid{unsigned(ntiles), unsigned(kv), 1u};
+  compact_count<<<grid, kCompactThreads, 0, s>>>(table, n, ntiles, cnt);
+  SP_LAUNCHED();
+  rc = exclusive_scan_u32(cnt, cnt, int64_t(cw), total, scan_ws, s);
+  if (rc) return rc;
+  compact_scatter<<<grid, kCompactThreads, 0, s>>>(table, n, ntiles, cnt, pos_out, val_out);
+  SP_LAUNCHED();
+  if (counts || npl) {
+    compact_counts<<<unsigned(cdiv(kv, 256)), 256, 0, s>>>(cnt, total, kv, ntiles, counts, npl,
+                                                          npl_limit);
+    SP_LAUNCHED();
+  }
+  return SP_OK;
+}
+
+int sp_native_to_tables(const int32_t* pair, int64_t kv, int64_t n_pairs, int32_t inverse,
+                        int64_t n_in, int64_t n_out, int32_t* pf, int32_t* pb, void* stream) {
+  SP_CHECK_ARG(kv >= 1 && n_pairs >= 0 && n_in >= 0 && n_out >= 0, "native_to_tables: bad sizes");
+  SP_CHECK_ARG(pair && pf, "native_to_tables: null pointer");
+  hipStream_t s = as_stream(stream);
+  int rc = launch_fill_i32(pf, kv * n_out, -1, s);
+  if (rc) return rc;
+  if (pb) {
+    rc = launch_fill_i32(pb, kv * n_in, -1, s);
+    if (rc) return rc;
+  }
+  if (kv * n_pairs == 0) return SP_OK;
+  const int32_t* pin = pair + (inverse ? kv * n_pairs : 0);
+  const int32_t* pout = pair + (inverse ? 0 : kv * n_pairs);
+  const int64_t blocks = cdiv(kv * n_pairs, 256);
+  SP_CHECK_ARG(blocks <= kMaxGridX, "native_to_tables: too large");
+  native_scatter<<<unsigned(blocks), 256, 0, s>>>(pin, pout, kv, n_pairs, n_in, n_out, pf, pb);
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,286 @@
+// Stable LSD radix sort and the mask-word split/sort entry point.
+//
+// Tile layout: a workgroup of 256 threads (4 waves) owns a tile of 2048
+// consecutive items, visited in 8 rounds; in round r wave w holds items
+// [r*256 + w*64, +64).  The 32 (round, wave) segments are in item order, so a
+// per-digit exclusive scan over them plus the in-wave peer rank gives a stable
+// local rank.  Global placement: exclusive scan over hist[digit][tile].
+#include "sp_sort.h"
+
+namespace sp {
+
+constexpr int kRsThreads = 256;
+constexpr int kRsRounds = 8;
+constexpr int kRsTile = kRsThreads * kRsRounds;  // 2048
+constexpr int kRsRadix = 256;
+constexpr int kRsSegs = kRsRounds * (kRsThreads / 64);  // 32
+
+struct RowWordDigit {
+  const uint32_t* words;
+  int mic;
+  int w;
+  uint32_t andmask;
+  int shift;
+  __device__ __forceinline__ uint32_t operator()(uint32_t row) const {
+    return ((words[int64_t(row) * mic + w] & andmask) >> shift) & 0xFFu;
+  }
+};
+
+struct KeyDigit32 {
+  int shift;
+  __device__ __forceinline__ uint32_t operator()(uint32_t k) const { return (k >> shift) & 0xFFu; }
+};
+
+struct KeyDigit64 {
+  int shift;
+  __device__ __forceinline__ uint32_t operator()(uint64_t k) const {
+    return uint32_t(k >> shift) & 0xFFu;
+  }
+};
+
+// Lanes of the wave holding the same 8-bit digit (restricted to `active`).
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t active) {
+  uint64_t peers = active;
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const bool bit = (d >> b) & 1u;
+    const uint64_t m = __ballot(bit);
+    peers &= bit ? m : ~m;
+  }
+  return peers;
+}
+
+template <class Item, class Digit>
+__global__ __launch_bounds__(kRsThreads) void rs_hist(const Item* __restrict__ in, int64_t n,
+                                                     Digit dig, uint32_t* __restrict__ hist,
+                                                     int64_t ntiles) {
+  __shared__ uint32_t cnt[kRsRadix];
+  cnt[threadIdx.x] = 0;
+  __syncthreads();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t base = int64_t(blockIdx.x) * kRsTile;
+#pragma unroll
+  for (int r = 0; r < kRsRounds; ++r) {
+    const int64_t idx = base + r * kRsThreads + wave * 64 + lane;
+    const bool valid = idx < n;
+    const uint32_t d = valid ? dig(in[idx]) : 0u;
+    const uint64_t peers = match_digit(d, __ballot(valid));
+    if (valid && (peers & lanemask_lt()) == 0) atomicAdd(&cnt[d], uint32_t(__popcll(peers)));
+  }
+  __syncthreads();
+  hist[int64_t(threadIdx.x) * ntiles + blockIdx.x] = cnt[threadIdx.x];
+}
+
+template <class Item, class Digit>
+__global__ __launch_bounds__(kRsThreads) void rs_scatter(const Item* __restrict__ in,
+                                                        Item* __restrict__ out, int64_t n,
+                                                        Digit dig,
+                                                        const uint32_t* __restrict__ offsets,
+                                                        int64_t ntiles) {
+  __shared__ uint32_t seg[kRsSegs][kRsRadix];
+  __shared__ uint32_t tile_base[kRsRadix];
+  for (int i = threadIdx.x; i < kRsSegs * kRsRadix; i += kRsThreads) (&seg[0][0])[i] = 0;
+  tile_base[threadIdx.x] = offsets[int64_t(threadIdx.x) * ntiles + blockIdx.x];
+  __syncthreads();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t base = int64_t(blockIdx.x) * kRsTile;
+  Item items[kRsRounds];
+  uint32_t digits[kRsRounds];
+  uint32_t ranks[kRsRounds];
+#pragma unroll
+  for (int r = 0; r < kRsRounds; ++r) {
+    const int64_t idx = base + r * kRsThreads + wave * 64 + lane;
+    const bool valid = idx < n;
+    items[r] = valid ? in[idx] : Item(0);
+    const uint32_t d = valid ? dig(items[r]) : 0u;
+    digits[r] = d;
+    const uint64_t peers = match_digit(d, __ballot(valid));
+    const uint64_t below = peers & lanemask_lt();
+    ranks[r] = uint32_t(__popcll(below));
+    if (valid && below == 0) seg[r * 4 + wave][d] = uint32_t(__popcll(peers));
+  }
+  __syncthreads();
+  {
+    uint32_t run = 0;
+    for (int s = 0; s < kRsSegs; ++s) {
+      const uint32_t c = seg[s][threadIdx.x];
+      seg[s][threadIdx.x] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kRsRounds; ++r) {
+    const int64_t idx = base + r * kRsThreads + wave * 64 + lane;
+    if (idx < n) {
+      const uint32_t d = digits[r];
+      out[tile_base[d] + seg[r * 4 + wave][d] + ranks[r]] = items[r];
+    }
+  }
+}
+
+__global__ void iota_u32(uint32_t* __restrict__ p, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = uint32_t(i);
+}
+
+struct RsBuffers {
+  uint32_t* hist;
+  void* scan_ws;
+};
+
+static size_t rs_hist_words(int64_t n) { return size_t(kRsRadix) * size_t(cdiv(n, kRsTile)); }
+
+template <class Item, class Digit>
+static int radix_pass(const Item* in, Item* out, int64_t n, Digit dig, const RsBuffers& b,
+                      hipStream_t s) {
+  const int64_t ntiles = cdiv(n, kRsTile);
+  SP_CHECK_ARG(ntiles <= kMaxGridX, "radix sort: %lld items exceed the grid limit", (long long)n);
+  rs_hist<Item, Digit><<<dim3(unsigned(ntiles)), dim3(kRsThreads), 0, s>>>(in, n, dig, b.hist,
+                                                                          ntiles);
+  SP_LAUNCHED();
+  int rc = exclusive_scan_u32(b.hist, b.hist, int64_t(kRsRadix) * ntiles, nullptr, b.scan_ws, s);
+  if (rc) return rc;
+  rs_scatter<Item, Digit><<<dim3(unsigned(ntiles)), dim3(kRsThreads), 0, s>>>(in, out, n, dig,
+                                                                             b.hist, ntiles);
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+template <class W>
+static void rows_layout(W& w, int64_t n) {
+  w.template take<uint32_t>(size_t(n));                  // perm A
+  w.template take<uint32_t>(size_t(n));                  // perm B
+  w.template take<uint32_t>(rs_hist_words(n));           // histograms
+  w.template take<char>(scan_workspace_bytes(int64_t(rs_hist_words(n))));
+}
+
+size_t sort_rows_ws_bytes(int64_t n) {
+  WsSizer z;
+  rows_layout(z, n);
+  return z.off;
+}
+
+int sort_rows_by_words(const uint32_t* words, int64_t n, int mic, int kv, uint32_t split,
+                       uint32_t** perm_out, void* ws, hipStream_t stream) {
+  WsCursor c(ws, ~size_t(0));
+  uint32_t* a = c.take<uint32_t>(size_t(n));
+  uint32_t* b = c.take<uint32_t>(size_t(n));
+  RsBuffers bufs;
+  bufs.hist = c.take<uint32_t>(rs_hist_words(n));
+  bufs.scan_ws = c.take<char>(scan_workspace_bytes(int64_t(rs_hist_words(n))));
+  iota_u32<<<dim3(unsigned(cdiv(n, 256))), dim3(256), 0, stream>>>(a, n);
+  SP_LAUNCHED();
+  for (int w = 0; w < mic; ++w) {
+    int bits = (w < mic - 1) ? 32 : kv - 32 * (mic - 1);
+    uint32_t andmask = 0xFFFFFFFFu;
+    if (w == 0) {
+      andmask = split;
+      const int top = split ? 32 - __builtin_clz(split) : 0;
+      bits = bits < top ? bits : top;
+    }
+    for (int shift = 0; shift < bits; shift += 8) {
+      RowWordDigit d{words, mic, w, andmask, shift};
+      int rc = radix_pass(a, b, n, d, bufs, stream);
+      if (rc) return rc;
+      uint32_t* t = a;
+      a = b;
+      b = t;
+    }
+  }
+  *perm_out = a;
+  return SP_OK;
+}
+
+template <class W>
+static void keys_layout(W& w, int64_t n) {
+  w.template take<uint32_t>(rs_hist_words(n));
+  w.template take<char>(scan_workspace_bytes(int64_t(rs_hist_words(n))));
+}
+
+size_t sort_keys_ws_bytes(int64_t n) {
+  WsSizer z;
+  keys_layout(z, n);
+  return z.off;
+}
+
+template <class Item, class Digit>
+static int sort_keys_impl(Item* keys, Item* tmp, int64_t n, int bits, Item** result, void* ws,
+                          hipStream_t stream) {
+  WsCursor c(ws, ~size_t(0));
+  RsBuffers bufs;
+  bufs.hist = c.take<uint32_t>(rs_hist_words(n));
+  bufs.scan_ws = c.take<char>(scan_workspace_bytes(int64_t(rs_hist_words(n))));
+  Item* a = keys;
+  Item* b = tmp;
+  for (int shift = 0; shift < bits; shift += 8) {
+    int rc = radix_pass(a, b, n, Digit{shift}, bufs, stream);
+    if (rc) return rc;
+    Item* t = a;
+    a = b;
+    b = t;
+  }
+  *result = a;
+  return SP_OK;
+}
+
+int sort_keys_u32(uint32_t* keys, uint32_t* tmp, int64_t n, int bits, uint32_t** result,
+                  void* ws, hipStream_t stream) {
+  return sort_keys_impl<uint32_t, KeyDigit32>(keys, tmp, n, bits, result, ws, stream);
+}
+
+int sort_keys_u64(uint64_t* keys, uint64_t* tmp, int64_t n, int bits, uint64_t** result,
+                  void* ws, hipStream_t stream) {
+  return sort_keys_impl<uint64_t, KeyDigit64>(keys, tmp, n, bits, result, ws, stream);
+}
+
+// pair_mask[i, w] = words[perm[i], w] (word 0 ANDed with split), argsort[i] = perm[i].
+__global__ void mask_gather(const uint32_t* __restrict__ words, const uint32_t* __restrict__ perm,
+                            int64_t n, int mic, uint32_t split, int32_t* __restrict__ pm,
+                            int32_t* __restrict__ args) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t row = perm ? perm[i] : uint32_t(i);
+  args[i] = int32_t(row);
+  for (int w = 0; w < mic; ++w) {
+    uint32_t v = words[int64_t(row) * mic + w];
+    if (w == 0) v &= split;
+    pm[i * mic + w] = int32_t(v);
+  }
+}
+
+}  // namespace sp
+
+using namespace sp;
+
+extern "C" {
+
+size_t sp_mask_sort_workspace_size(int64_t n, int32_t mic) {
+  (void)mic;
+  return sort_rows_ws_bytes(n > 0 ? n : 1);
+}
+
+int sp_mask_sort(const uint32_t* words, int64_t n, int32_t mic, int32_t kv, uint32_t split_mask,
+                 int32_t do_sort, int32_t* pair_mask, int32_t* argsort, void* ws, size_t ws_bytes,
+                 void* stream) {
+  hipStream_t s = as_stream(stream);
+  SP_CHECK_ARG(n >= 0 && mic >= 1 && kv >= 1 && kv <= 32 * mic, "mask_sort: bad sizes n=%lld mic=%d kv=%d",
+               (long long)n, mic, kv);
+  if (n == 0) return SP_OK;
+  SP_CHECK_ARG(words && pair_mask && argsort, "mask_sort: null pointer");
+  SP_CHECK_ARG(n < (int64_t(1) << 31), "mask_sort: n too large");
+  uint32_t* perm = nullptr;
+  if (do_sort) {
+    if (ws_bytes < sort_rows_ws_bytes(n) || !ws)
+      return set_error(SP_ERR_WORKSPACE, "mask_sort: workspace %zu < %zu", ws_bytes,
+                       sort_rows_ws_bytes(n));
+    int rc = sort_rows_by_words(words, n, mic, kv, split_mask, &perm, ws, s);
+    if (rc) return rc;
+  }
+  mask_gather<<<dim3(unsigned(cdiv(n, 256))), dim3(256), 0, s>>>(words, perm, n, mic, split_mask,
+                                                                 pair_mask, argsort);
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+}  // extern "C"

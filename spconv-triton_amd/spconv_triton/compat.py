@@ -1,0 +1,25 @@
+"""Stand-in for the ``cumm.tensorview`` activation enum that spconv's API exposes.
+
+``from spconv_triton.compat import tv; tv.gemm.Activation.ReLU`` works as in
+spconv, without cumm.
+"""
+
+from enum import Enum
+
+
+class Activation(Enum):
+    None_ = 0
+    ReLU = 1
+    Sigmoid = 2
+    LeakyReLU = 3
+
+
+class _Gemm:
+    Activation = Activation
+
+
+class _TensorView:
+    gemm = _Gemm
+
+
+tv = _TensorView()

@@ -1,0 +1,207 @@
+"""Gather-GEMM host wrappers (forward, input gradient, weight gradient).
+
+Host-side mirror of ``spconv_triton/pytorch/_impl/gemm.py`` of the reference
+(``conv_forward`` :501-568, ``conv_backward_input`` :571-631,
+``conv_backward_weight`` :634-713).  The device work is the MFMA gather-GEMM of
+``csrc/sp_gemm.hip``.
+
+Precision: every GEMM accumulates in fp32 on the matrix cores.  The
+reference's optional fp16 accumulation (``SPCONV_ALLOW_FP16_ACCUM`` /
+``fp32_accum=False``) and TF32 (``SPCONV_ALLOW_TF32``) are speed knobs that
+relax precision; on gfx950 there is no fp16-accumulating or xf32 MFMA, so
+both requests are served at full fp32 accumulation / IEEE fp32, which is at
+least as accurate.  The flags are still accepted.
+"""
+
+from __future__ import annotations
+
+import weakref
+
+import torch
+
+from . import _lib
+
+
+def _should_mask(kv: int, pmask, argsort) -> bool:
+    """Masked path applies only to single-word masks, 1 < kv <= 32 (reference gemm.py:486-498)."""
+    return pmask is not None and argsort is not None and 1 < kv <= 32
+
+
+class _PackCache:
+    """Packed weights per weight tensor, valid while the tensor's storage,
+    version counter (bumped by in-place updates such as optimizer steps) and
+    the bias are unchanged."""
+
+    def __init__(self):
+        self._store = weakref.WeakKeyDictionary()
+
+    @staticmethod
+    def _stamp(w: torch.Tensor, bias: torch.Tensor | None):
+        bstamp = None if bias is None else (bias.data_ptr(), bias._version, bias.dtype)
+        return (w.data_ptr(), w._version, w.dtype, tuple(w.shape), bstamp)
+
+    def get(self, w, bias, dtype, transpose):
+        try:
+            per = self._store.get(w)
+        except TypeError:
+            return None
+        if per is None:
+            return None
+        hit = per.get((dtype, transpose))
+        if hit is not None and hit[0] == self._stamp(w, bias):
+            return hit[1]
+        return None
+
+    def put(self, w, bias, dtype, transpose, packed):
+        try:
+            per = self._store.setdefault(w, {})
+        except TypeError:
+            return
+        per[(dtype, transpose)] = (self._stamp(w, bias), packed)
+
+
+_PACKED = _PackCache()
+
+
+def packed_weight(filters: torch.Tensor, bias: torch.Tensor | None, dtype: torch.dtype,
+                  transpose: bool) -> torch.Tensor:
+    """Weights (+ bias) relaid into the MFMA operand layout of ``dtype``; see
+    ``sp_conv_pack_weight``.  filters is KRSC [K, *ksize, C]."""
+    hit = _PACKED.get(filters, bias, dtype, transpose)
+    if hit is not None:
+        return hit
+    K, C = filters.shape[0], filters.shape[-1]
+    w = filters.detach().reshape(K, -1, C).contiguous()
+    kv = w.shape[1]
+    b = None if bias is None else bias.detach().contiguous()
+    if b is not None and b.dtype != w.dtype:
+        b = b.to(w.dtype)
+    L = _lib.lib()
+    dt = _lib.dtype_code(dtype)
+    packed = torch.empty(L.sp_conv_packed_bytes(K, kv, C, dt, int(transpose)), dtype=torch.uint8,
+                         device=w.device)
+    _lib.check(L.sp_conv_pack_weight(_lib.ptr(w), _lib.dtype_code(w.dtype), _lib.ptr(b), K, kv,
+                                     C, dt, int(transpose), _lib.ptr(packed),
+                                     _lib.stream_of(w.device)), "sp_conv_pack_weight")
+    _PACKED.put(filters, bias, dtype, transpose, packed)
+    return packed
+
+
+def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: torch.Tensor,
+          M: int, pm, ar, out: torch.Tensor):
+    K, C = filters.shape[0], filters.shape[-1]
+    kv = pairs.shape[0]
+    packed = packed_weight(filters, bias, a.dtype, transpose)
+    _lib.check(_lib.lib().sp_conv_gemm_packed(
+        _lib.ptr(a), _lib.dtype_code(a.dtype), a.shape[0], _lib.ptr(packed), K, kv, C,
+        int(transpose), int(bias is not None), _lib.ptr(pairs), M, _lib.ptr(pm), _lib.ptr(ar),
+        _lib.ptr(out), _lib.dtype_code(out.dtype), _lib.stream_of(a.device)),
+        "sp_conv_gemm_packed")
+
+
+def conv_forward(features: torch.Tensor, filters_krsc: torch.Tensor, pair_fwd: torch.Tensor,
+                 n_out: int, bias: torch.Tensor | None = None,
+                 out_dtype: torch.dtype | None = None, pair_mask: torch.Tensor | None = None,
+                 mask_argsort: torch.Tensor | None = None,
+                 fp32_accum: bool | None = None) -> torch.Tensor:
+    """Gather-GEMM forward; returns [n_out, K].  filters_krsc is [K, kv, C]
+    (or the KRSC parameter [K, *ksize, C] itself, which lets packed weights be
+    reused across calls)."""
+    _lib.require_gpu(features, pair_fwd)
+    K, C = filters_krsc.shape[0], filters_krsc.shape[-1]
+    kv = pair_fwd.shape[0]
+    if out_dtype is None:
+        out_dtype = features.dtype
+    out = torch.empty((n_out, K), dtype=out_dtype, device=features.device)
+    if n_out == 0:
+        return out
+    if filters_krsc.numel() != K * kv * C:
+        raise AssertionError("filters do not match the pair table's kernel volume")
+    x = features.contiguous()
+    pf = pair_fwd.contiguous()
+    if pf.shape != (kv, n_out):
+        raise AssertionError(f"pair_fwd shape {tuple(pf.shape)} != ({kv}, {n_out})")
+    if x.shape[1] != C:
+        raise AssertionError("channel size mismatch")
+    use_mask = _should_mask(kv, pair_mask, mask_argsort)
+    pm = pair_mask.contiguous() if use_mask else None
+    ar = mask_argsort.contiguous() if use_mask else None
+    if use_mask and (pm.numel() != n_out or ar.numel() != n_out):
+        raise AssertionError("mask tables do not match the output rows")
+    _gemm(x, filters_krsc, bias, False, pf, n_out, pm, ar, out)
+    return out
+
+
+def conv_backward_input(grad_out: torch.Tensor, filters_krsc: torch.Tensor,
+                        pair_bwd: torch.Tensor, n_in: int,
+                        pair_mask: torch.Tensor | None = None,
+                        mask_argsort: torch.Tensor | None = None,
+                        fp32_accum: bool | None = None) -> torch.Tensor:
+    """din[j, c] = sum_k grad_out[pair_bwd[k, j], :] @ W[k][:, c]; returns [n_in, C]."""
+    _lib.require_gpu(grad_out, pair_bwd)
+    K, C = filters_krsc.shape[0], filters_krsc.shape[-1]
+    kv = pair_bwd.shape[0]
+    din = torch.empty((n_in, C), dtype=grad_out.dtype, device=grad_out.device)
+    if n_in == 0:
+        return din
+    g = grad_out.contiguous()
+    pb = pair_bwd.contiguous()
+    if pb.shape != (kv, n_in):
+        raise AssertionError(f"pair_bwd shape {tuple(pb.shape)} != ({kv}, {n_in})")
+    if g.shape[1] != K:
+        raise AssertionError("grad_out channels do not match the filters")
+    use_mask = _should_mask(kv, pair_mask, mask_argsort)
+    pm = pair_mask.contiguous() if use_mask else None
+    ar = mask_argsort.contiguous() if use_mask else None
+    _gemm(g, filters_krsc, None, True, pb, n_in, pm, ar, din)
+    return din
+
+
+def compacted_signal(pair_fwd: torch.Tensor):
+    """Per-offset (input row, output row) lists of a gather table, output rows
+    ascending -- the reference's ``valid_signal`` (gemm.py:661-669) in a
+    per-offset slotted layout.  Memoised on the table tensor."""
+    cached = getattr(pair_fwd, "_spconv_triton_dw_sig", None)
+    if cached is not None:
+        return cached
+    pf = pair_fwd.contiguous()
+    kv, n = pf.shape
+    device = pf.device
+    out_rows = torch.empty((kv, n), dtype=torch.int32, device=device)
+    in_rows = torch.empty((kv, n), dtype=torch.int32, device=device)
+    counts = torch.empty((kv,), dtype=torch.int32, device=device)
+    L = _lib.lib()
+    ws = _lib.workspace(L.sp_compact_workspace_size(kv, n), device)
+    _lib.check(L.sp_compact_table(_lib.ptr(pf), kv, n, _lib.ptr(out_rows), _lib.ptr(in_rows),
+                                  _lib.ptr(counts), None, kv, _lib.ptr(ws), ws.numel(),
+                                  _lib.stream_of(device)), "sp_compact_table")
+    sig = (in_rows, out_rows, counts)
+    pair_fwd._spconv_triton_dw_sig = sig
+    return sig
+
+
+def conv_backward_weight(features: torch.Tensor, grad_out: torch.Tensor, pair_fwd: torch.Tensor,
+                         weight_shape_krsc, fp32_accum: bool | None = None) -> torch.Tensor:
+    """dW [K, kv, C] = per-offset X^T G over compacted pairs (deterministic split-P)."""
+    _lib.require_gpu(features, grad_out, pair_fwd)
+    K, C = int(weight_shape_krsc[0]), int(weight_shape_krsc[-1])
+    kv = int(pair_fwd.shape[0])
+    n_out = grad_out.shape[0]
+    dw = torch.empty((K, kv, C), dtype=grad_out.dtype, device=grad_out.device)
+    if n_out == 0 or kv == 0:
+        dw.zero_()
+        return dw
+    x = features.contiguous()
+    g = grad_out.contiguous()
+    if x.dtype != g.dtype:
+        raise AssertionError("features and grad_out dtypes differ")
+    in_rows, out_rows, counts = compacted_signal(pair_fwd)
+    stride = in_rows.shape[1]
+    L = _lib.lib()
+    ws = _lib.workspace(L.sp_wgrad_workspace_size(K, kv, C, stride), x.device)
+    _lib.check(L.sp_conv_wgrad(_lib.ptr(x), x.shape[0], _lib.ptr(g), n_out,
+                               _lib.dtype_code(x.dtype), C, K, kv, _lib.ptr(in_rows),
+                               _lib.ptr(out_rows), _lib.ptr(counts), stride, _lib.ptr(dw),
+                               _lib.ptr(ws), ws.numel(), _lib.stream_of(x.device)),
+               "sp_conv_wgrad")
+    return dw

@@ -1,0 +1,14 @@
+"""Torch version as a list of ints (spconv.pytorch.constants)."""
+
+import torch
+
+
+def _parse(version: str) -> list[int]:
+    core = version.split("+")[0].split(".dev")[0]
+    try:
+        return [int(p) for p in core.split(".")[:3]]
+    except ValueError:
+        return [1, 8, 0]
+
+
+PYTORCH_VERSION: list[int] = _parse(str(torch.__version__))

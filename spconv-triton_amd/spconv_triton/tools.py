@@ -1,0 +1,25 @@
+"""Timer stand-in with spconv's ``CUDAKernelTimer`` interface (records nothing).
+
+Per-kernel timing on MI355X comes from ``rocprofv3 --kernel-trace``.
+"""
+
+import contextlib
+
+CPU_ONLY_BUILD = False
+
+
+class CUDAKernelTimer:
+    def __init__(self, enable: bool = True):
+        self.enable = enable
+        self._timer = None
+
+    @contextlib.contextmanager
+    def namespace(self, name: str):
+        yield
+
+    @contextlib.contextmanager
+    def record(self, name: str, stream: int = 0):
+        yield
+
+    def get_all_pair_time(self):
+        return {}

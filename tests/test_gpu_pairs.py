@@ -1,0 +1,288 @@
+"""GPU parity of rulebook generation: HIP hash pair generator vs the CPU oracle.
+
+Everything here is integer work, so the bar is bit-exact: output coordinates
+and their order, pair_fwd / pair_bwd tables, Native [2, kv, N] lists and npl,
+sorted mask words and mask argsort (reference ``_impl/pairs.py``).
+Covers subm / strided / dilated / transposed geometries in 1-4 D, kv up to 125
+(multi-word masks), MaskSplit, num_out_act_bound, the int64 key path (with an
+int32 translation-invariance check), batch independence and the error cases.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+# (spatial shape, ksize, stride, padding, dilation, out_padding, subm, transpose)
+GEOMS = [
+    ([20, 18, 16], [3, 3, 3], [1] * 3, [1] * 3, [1] * 3, [0] * 3, True, False),
+    ([20, 18, 16], [3, 1, 5], [1] * 3, [0] * 3, [2, 1, 1], [0] * 3, True, False),
+    ([20, 18, 16], [3, 3, 3], [2] * 3, [1] * 3, [1] * 3, [0] * 3, False, False),
+    ([20, 18, 16], [2, 3, 2], [2, 1, 3], [0, 1, 1], [1, 2, 1], [0] * 3, False, False),
+    ([12, 10, 14], [3, 3, 3], [2] * 3, [1] * 3, [1] * 3, [1, 0, 1], False, True),
+    ([12, 10, 14], [2, 2, 2], [2] * 3, [0] * 3, [1] * 3, [0] * 3, False, True),
+    ([40, 36], [3, 3], [2, 2], [1, 1], [1, 1], [0, 0], False, False),
+    ([40, 36], [5, 5], [1, 1], [2, 2], [1, 1], [0, 0], True, False),
+    ([300], [3], [1], [1], [1], [0], True, False),
+    ([300], [4], [3], [1], [1], [0], False, False),
+    ([10, 8, 7, 6], [3, 3, 3, 3], [1] * 4, [1] * 4, [1] * 4, [0] * 4, True, False),
+    ([16, 16, 16], [5, 5, 5], [1] * 3, [2] * 3, [1] * 3, [0] * 3, True, False),
+    ([16, 16, 16], [5, 5, 5], [2] * 3, [2] * 3, [1] * 3, [0] * 3, False, False),
+    ([16, 16, 16], [2, 2, 2], [2] * 3, [0] * 3, [1] * 3, [0] * 3, False, False),
+]
+
+
+def rand_indices(rng, batch, shape, n):
+    vol = int(np.prod(shape))
+    rows = []
+    for b in range(batch):
+        lin = rng.choice(vol, size=min(n, vol), replace=False)
+        c = np.stack(np.unravel_index(lin, shape), 1)
+        rows.append(np.concatenate([np.full((c.shape[0], 1), b), c], 1))
+    idx = np.concatenate(rows, 0).astype(np.int32)
+    return idx[rng.permutation(idx.shape[0])]
+
+
+def _eq(a, b, what):
+    a = a.detach().cpu().numpy() if isinstance(a, torch.Tensor) else np.asarray(a)
+    b = np.asarray(b)
+    assert a.shape == b.shape, f"{what}: shape {a.shape} != {b.shape}"
+    bad = int((a != b).sum())
+    assert bad == 0, f"{what}: {bad}/{a.size} entries differ"
+
+
+def _igemm(idx, batch, g, is_train, split=False, bound=-1):
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+
+    shape, ks, st, pad, dil, op, subm, tr = g
+    algo = ConvAlgo.MaskSplitImplicitGemm if split else ConvAlgo.MaskImplicitGemm
+    t = torch.from_numpy(idx).to(DEV)
+    res = ops.get_indice_pairs_implicit_gemm(t, batch, shape, algo, ks, st, pad, dil, op, subm,
+                                             tr, is_train=is_train, num_out_act_bound=bound)
+    exp = orc.igemm_pairs(idx, batch, shape, ks, st, pad, dil, op, subm, tr, is_train,
+                          is_mask_split=split, num_out_act_bound=bound)
+    return res, exp, t
+
+
+def _compare_igemm(res, exp, t, subm, is_train):
+    if subm:
+        assert res[0] is t, "subm must return the input indices object"
+    else:
+        _eq(res[0], exp[0], "out_indices")
+    _eq(res[1], exp[1], "indice_num_per_loc")
+    _eq(res[2], exp[2], "pair_fwd")
+    if is_train:
+        _eq(res[3], exp[3], "pair_bwd")
+    else:
+        assert res[3].numel() == 0
+    for name, i in (("pair_mask_fwd", 4), ("pair_mask_bwd", 5), ("mask_argsort_fwd", 6),
+                    ("mask_argsort_bwd", 7)):
+        assert len(res[i]) == len(exp[i]), name
+        for a, b in zip(res[i], exp[i]):
+            _eq(a, b, name)
+    assert [int(m[0]) for m in res[8]] == [int(m[0]) for m in exp[8]]
+
+
+@pytest.mark.parametrize("is_train", [True, False])
+@pytest.mark.parametrize("gi", range(len(GEOMS)))
+def test_igemm_pairs_bit_exact(gi, is_train):
+    g = GEOMS[gi]
+    rng = np.random.default_rng(1000 + gi)
+    idx = rand_indices(rng, 3, g[0], max(8, int(np.prod(g[0])) // 5))
+    res, exp, t = _igemm(idx, 3, g, is_train)
+    _compare_igemm(res, exp, t, g[6], is_train)
+
+
+@pytest.mark.parametrize("gi", [0, 2, 3, 6, 7])
+def test_mask_split_bit_exact(gi):
+    g = GEOMS[gi]
+    rng = np.random.default_rng(2000 + gi)
+    idx = rand_indices(rng, 2, g[0], int(np.prod(g[0])) // 4)
+    res, exp, t = _igemm(idx, 2, g, True, split=True)
+    _compare_igemm(res, exp, t, g[6], True)
+
+
+def test_mask_split_kv_over_32_raises():
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+
+    idx = torch.from_numpy(rand_indices(np.random.default_rng(1), 1, [16] * 3, 300)).to(DEV)
+    with pytest.raises(AssertionError, match="Not Implemented"):
+        ops.get_indice_pairs_implicit_gemm(idx, 1, [16] * 3, ConvAlgo.MaskSplitImplicitGemm,
+                                           [5] * 3, [1] * 3, [2] * 3, [1] * 3, [0] * 3, True)
+
+
+@pytest.mark.parametrize("gi", [2, 4, 6, 12])
+def test_num_out_act_bound(gi):
+    g = GEOMS[gi]
+    rng = np.random.default_rng(3000 + gi)
+    idx = rand_indices(rng, 2, g[0], int(np.prod(g[0])) // 5)
+    full = orc.igemm_pairs(idx, 2, *g[:8], True)
+    bound = max(1, full[0].shape[0] // 3)
+    res, exp, t = _igemm(idx, 2, g, True, bound=bound)
+    assert res[0].shape[0] == bound
+    _compare_igemm(res, exp, t, g[6], True)
+
+
+@pytest.mark.parametrize("gi", range(len(GEOMS)))
+def test_native_pairs_bit_exact(gi):
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+
+    shape, ks, st, pad, dil, op, subm, tr = GEOMS[gi]
+    rng = np.random.default_rng(4000 + gi)
+    idx = rand_indices(rng, 2, shape, max(8, int(np.prod(shape)) // 5))
+    t = torch.from_numpy(idx).to(DEV)
+    out_inds, pair, npl = ops.get_indice_pairs(t, 2, shape, ConvAlgo.Native, ks, st, pad, dil,
+                                               op, subm, tr)
+    e_inds, e_pair, e_npl = orc.native_pairs(idx, 2, shape, ks, st, pad, dil, op, subm, tr)
+    _eq(out_inds, e_inds, "out_indices")
+    _eq(pair, e_pair, "pair")
+    _eq(npl, e_npl, "indice_num_per_loc")
+    # native -> gather tables, forward and inverse
+    from spconv_triton.pytorch._impl import pairs as P
+
+    n_out = out_inds.shape[0]
+    pf, pb = P.native_pair_to_tables(pair, npl, idx.shape[0], n_out, False)
+    e_pf, e_pb = orc.native_pair_to_tables(e_pair, idx.shape[0], n_out, False)
+    _eq(pf, e_pf, "native pf")
+    _eq(pb, e_pb, "native pb")
+    ipf, ipb = P.native_pair_to_tables(pair, npl, n_out, idx.shape[0], True)
+    _eq(ipf, e_pb, "inverse pf")
+    _eq(ipb, e_pf, "inverse pb")
+    # memoised
+    pf2, _ = P.native_pair_to_tables(pair, npl, idx.shape[0], n_out, False)
+    assert pf2 is pf
+
+
+def _place(idx, offset):
+    out = idx.copy()
+    out[:, 1:] += np.asarray(offset, np.int32)
+    return out
+
+
+@pytest.mark.parametrize("subm", [True, False])
+def test_int64_keys_match_oracle_and_int32_translation(subm):
+    """Grid volume >= 2^31 selects 64-bit keys; tables equal the oracle's and
+    the same cloud placed in a small (int32) grid (reference
+    tests/test_int64_linearize.py:70-120)."""
+    from spconv_triton.pytorch._impl import pairs as P
+
+    rng = np.random.default_rng(7)
+    small = [24, 24, 24]
+    idx = rand_indices(rng, 2, small, 2500)
+    big_shape = [4096, 2048, 1024]
+    off = [2048, 1024, 512]
+    big = _place(idx, off)
+    st = [1] * 3 if subm else [2] * 3
+    g_small = (small, [3] * 3, st, [1] * 3, [1] * 3, [0] * 3, subm, False)
+    g_big = (big_shape, [3] * 3, st, [1] * 3, [1] * 3, [0] * 3, subm, False)
+    assert P.key_is_int64(2, big_shape, big_shape, subm)
+    assert not P.key_is_int64(2, small, small, subm)
+    res_b, exp_b, tb = _igemm(big, 2, g_big, True)
+    _compare_igemm(res_b, exp_b, tb, subm, True)
+    res_s, _, _ = _igemm(idx, 2, g_small, True)
+    for i in (2, 3):
+        _eq(res_b[i], res_s[i].cpu().numpy(), f"table {i} int64 vs int32")
+    for i in (4, 5, 6, 7):
+        for a, b in zip(res_b[i], res_s[i]):
+            _eq(a, b.cpu().numpy(), f"mask {i} int64 vs int32")
+    if not subm:
+        shift = np.asarray([0] + [o // 2 for o in off], np.int32)
+        _eq(res_b[0], res_s[0].cpu().numpy() + shift, "out_indices int64 vs int32")
+
+
+def test_batches_are_independent():
+    """Pairs of a multi-batch tensor equal the per-batch pairs (reference
+    tests/test_large_batch.py:94-154)."""
+    rng = np.random.default_rng(11)
+    shape = [18, 18, 18]
+    idx = rand_indices(rng, 4, shape, 900)
+    g = (shape, [3] * 3, [2] * 3, [1] * 3, [1] * 3, [0] * 3, False, False)
+    res, exp, t = _igemm(idx, 4, g, True)
+    _compare_igemm(res, exp, t, False, True)
+    out = res[0].cpu().numpy()
+    assert (np.diff(out[:, 0]) >= 0).all(), "outputs grouped by batch"
+    for b in range(4):
+        sel = idx[:, 0] == b
+        sub = idx[sel].copy()
+        sub[:, 0] = 0
+        r1, _, _ = _igemm(sub, 1, g, True)
+        mine = out[out[:, 0] == b].copy()
+        mine[:, 0] = 0
+        _eq(r1[0], mine, f"batch {b} outputs")
+
+
+def test_pairgen_deterministic():
+    rng = np.random.default_rng(5)
+    shape = [32, 32, 32]
+    idx = rand_indices(rng, 2, shape, 5000)
+    g = (shape, [3] * 3, [2] * 3, [1] * 3, [1] * 3, [0] * 3, False, False)
+    a, _, _ = _igemm(idx, 2, g, True)
+    b, _, _ = _igemm(idx, 2, g, True)
+    for i in (0, 2, 3):
+        assert torch.equal(a[i], b[i])
+
+
+def test_errors():
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+
+    empty = torch.zeros((0, 4), dtype=torch.int32, device=DEV)
+    with pytest.raises(ValueError):
+        ops.get_indice_pairs_implicit_gemm(empty, 1, [8] * 3, ConvAlgo.MaskImplicitGemm,
+                                           [3] * 3, [1] * 3, [1] * 3, [1] * 3, [0] * 3, True)
+    one = torch.tensor([[0, 1, 1, 1]], dtype=torch.int32, device=DEV)
+    with pytest.raises(NotImplementedError):
+        ops.get_indice_pairs_implicit_gemm(one, 1, [8] * 3, ConvAlgo.MaskImplicitGemm, [2] * 3,
+                                           [1] * 3, [0] * 3, [1] * 3, [0] * 3, True)
+    # every candidate falls outside: "points vanished"
+    with pytest.raises(ValueError, match="vanished"):
+        ops.get_indice_pairs_implicit_gemm(one, 1, [8] * 3, ConvAlgo.MaskImplicitGemm, [3] * 3,
+                                           [4] * 3, [0] * 3, [1] * 3, [0] * 3, False)
+    with pytest.raises(ValueError, match="reach zero"):
+        ops.get_indice_pairs_implicit_gemm(one, 1, [2] * 3, ConvAlgo.MaskImplicitGemm, [5] * 3,
+                                           [1] * 3, [0] * 3, [1] * 3, [0] * 3, False)
+
+
+def test_large_subm_properties():
+    """200k-voxel surface-like cloud: subm table invariants that hold at any size
+    (centre offset is the identity; pair_bwd is pair_fwd with offsets reversed;
+    masks sorted and argsort a permutation; bits equal the table)."""
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+
+    from bench_data import surface_cloud
+
+    idx = surface_cloud(200_000, 256, seed=0)
+    t = torch.from_numpy(idx).to(DEV)
+    res = ops.get_indice_pairs_implicit_gemm(t, 1, [256] * 3, ConvAlgo.MaskImplicitGemm,
+                                             [3] * 3, [1] * 3, [1] * 3, [1] * 3, [0] * 3, True,
+                                             is_train=True)
+    pf, pb = res[2], res[3]
+    n = idx.shape[0]
+    assert torch.equal(pf[13], torch.arange(n, dtype=torch.int32, device=DEV))
+    assert torch.equal(pb, pf.flip(0))
+    pm, ar = res[4][0][:, 0], res[6][0]
+    words = pm.long() & 0xFFFFFFFF
+    assert bool((words[1:] >= words[:-1]).all())
+    assert torch.equal(torch.sort(ar.long())[0], torch.arange(n, device=DEV))
+    bits = ((pf >= 0).long() << torch.arange(27, device=DEV)[:, None]).sum(0)
+    assert torch.equal(bits[ar.long()], words)
+    # spot-check against the oracle on a 20k subset of rows' neighbourhoods
+    sub = idx[:20000]
+    exp = orc.igemm_pairs(sub, 1, [256] * 3, [3] * 3, [1] * 3, [1] * 3, [1] * 3, [0] * 3, True,
+                          False, True)
+    r2 = ops.get_indice_pairs_implicit_gemm(torch.from_numpy(sub).to(DEV), 1, [256] * 3,
+                                            ConvAlgo.MaskImplicitGemm, [3] * 3, [1] * 3, [1] * 3,
+                                            [1] * 3, [0] * 3, True, is_train=True)
+    _eq(r2[2], exp[2], "pair_fwd 20k")
+    _eq(r2[3], exp[3], "pair_bwd 20k")
+    _eq(r2[4][0], exp[4][0], "pair_mask 20k")
+    _eq(r2[6][0], exp[6][0], "mask_argsort 20k")
