@@ -346,7 +346,8 @@ static Packed packed_layout(int64_t K, int64_t kv, int64_t C, int dtype, int tra
   Packed p;
   p.N = int(transpose ? C : K);
   p.R = int(transpose ? K : C);
-  p.Rp = int(padded(p.R, vec_of(dtype)));
+  // the reduction runs in MFMA steps of 2 * V (two lane halves of V each)
+  p.Rp = int(padded(p.R, 2 * vec_of(dtype)));
   p.bt_bytes = size_t(kv) * size_t(p.Rp) * size_t(p.N) * size_t(elem_size(dtype));
   p.bias_off = align_up(p.bt_bytes, 256);
   p.total = p.bias_off + align_up(size_t(p.N) * sizeof(float), 256);

@@ -92,6 +92,9 @@ template <typename T>
 __global__ __launch_bounds__(256) void avgpool_bwd_kernel(
     const T* __restrict__ g, const int32_t* __restrict__ count, int64_t n_out, int64_t C,
     const int32_t* __restrict__ pb, int64_t kv, int64_t n_in, T* __restrict__ dx) {
+  // product and sum rounded separately, like the reference's
+  // acc += where(ok, g * cnt, 0): no fused multiply-add here
+#pragma clang fp contract(off)
   using A = typename Acc<T>::type;
   const int64_t j = int64_t(blockIdx.x) * 4 + threadIdx.y;
   const int64_t c = int64_t(blockIdx.y) * 64 + threadIdx.x;

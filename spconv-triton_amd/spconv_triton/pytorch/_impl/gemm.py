@@ -30,10 +30,11 @@ def _should_mask(kv: int, pmask, argsort) -> bool:
 class _PackCache:
     """Packed weights per weight tensor, valid while the tensor's storage,
     version counter (bumped by in-place updates such as optimizer steps) and
-    the bias are unchanged."""
+    the bias are unchanged.  Keyed by object identity; an entry is dropped
+    when its weight tensor is freed."""
 
     def __init__(self):
-        self._store = weakref.WeakKeyDictionary()
+        self._store = {}
 
     @staticmethod
     def _stamp(w: torch.Tensor, bias: torch.Tensor | None):
@@ -41,23 +42,23 @@ class _PackCache:
         return (w.data_ptr(), w._version, w.dtype, tuple(w.shape), bstamp)
 
     def get(self, w, bias, dtype, transpose):
-        try:
-            per = self._store.get(w)
-        except TypeError:
+        ent = self._store.get(id(w))
+        if ent is None or ent[0]() is not w:
             return None
-        if per is None:
-            return None
-        hit = per.get((dtype, transpose))
+        hit = ent[1].get((dtype, transpose))
         if hit is not None and hit[0] == self._stamp(w, bias):
             return hit[1]
         return None
 
     def put(self, w, bias, dtype, transpose, packed):
-        try:
-            per = self._store.setdefault(w, {})
-        except TypeError:
-            return
-        per[(dtype, transpose)] = (self._stamp(w, bias), packed)
+        key = id(w)
+        ent = self._store.get(key)
+        if ent is None or ent[0]() is not w:
+            store = self._store
+            ref = weakref.ref(w, lambda _r, k=key, s=store: s.pop(k, None))
+            ent = (ref, {})
+            store[key] = ent
+        ent[1][(dtype, transpose)] = (self._stamp(w, bias), packed)
 
 
 _PACKED = _PackCache()
