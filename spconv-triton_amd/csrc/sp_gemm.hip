@@ -134,108 +134,7 @@ __device__ __forceinline__ typename Mfma<T>::frag load_frag_vec(const T* p) {
   return *reinterpret_cast<const typename Mfma<T>::frag*>(p);
 }
 
-template <typename T, typename OutT, bool MASK, bool VEC>
-__global__ __launch_bounds__(256) void gather_gemm(
-    const T* __restrict__ A, int64_t n_src, const T* __restrict__ Bt,
-    const int32_t* __restrict__ pairs, const int32_t* __restrict__ pmask,
-    const int32_t* __restrict__ argsort, const float* __restrict__ bias, OutT* __restrict__ out,
-    int64_t M, int N, int R, int Rp, int kv) {
-  using MF = Mfma<T>;
-  using frag = typename MF::frag;
-  constexpr int V = MF::V;
-  constexpr int KSTEP = MF::KSTEP;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int h = lane >> 5, l32 = lane & 31;
-  const int64_t slot0 = (int64_t(blockIdx.x) * 4 + wave) * 64;
-  if (slot0 >= M) return;  // whole wave idle; no workgroup barrier below
-  const int n0 = blockIdx.y * 64;
-
-  int64_t rm[2];
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const int64_t slot = slot0 + mt * 32 + l32;
-    rm[mt] = slot < M ? (MASK ? int64_t(argsort[slot]) : slot) : -1;
-    if (rm[mt] >= M) rm[mt] = -1;
-  }
-  uint32_t tmask = 0xFFFFFFFFu;
-  if (MASK) {
-    const int64_t slot = slot0 + lane;
-    tmask = wave_or(slot < M ? uint32_t(pmask[slot]) : 0u);
-  }
-
-  floatx16 acc[2][2];
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.f;
-
-  const int64_t bk_stride = int64_t(Rp / V) * N * V;  // elements per offset in Bt
-  for (int k = 0; k < kv; ++k) {
-    if (MASK && !((tmask >> k) & 1u)) continue;
-    int64_t src[2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      int32_t j = rm[mt] >= 0 ? pairs[int64_t(k) * M + rm[mt]] : -1;
-      src[mt] = (j >= 0 && j < n_src) ? int64_t(j) : -1;
-    }
-    const T* bbase = Bt + int64_t(k) * bk_stride;
-    for (int r0 = 0; r0 < Rp; r0 += KSTEP) {
-      const int rr = r0 + h * V;
-      frag a[2], b[2];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        if (VEC) {
-          if (src[mt] >= 0 && rr < R) {
-            a[mt] = load_frag_vec<T>(A + src[mt] * R + rr);
-          } else {
-#pragma unroll
-            for (int e = 0; e < V; ++e) a[mt][e] = T(0.f);
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < V; ++e)
-            a[mt][e] = (src[mt] >= 0 && rr + e < R) ? A[src[mt] * R + rr + e] : T(0.f);
-        }
-      }
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int col = n0 + nt * 32 + l32;
-        if (col < N) {
-          b[nt] = load_frag_vec<T>(bbase + (int64_t(rr / V) * N + col) * V);
-        } else {
-#pragma unroll
-          for (int e = 0; e < V; ++e) b[nt][e] = T(0.f);
-        }
-      }
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) MF::mma(a[mt], b[nt], acc[mt][nt]);
-    }
-  }
-
-  // epilogue: lane l holds column l%32 of rows 8*(i/4) + 4*h + (i%4)
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int rloc = (i >> 2) * 8 + h * 4 + (i & 3);
-      const int64_t row = __shfl(rm[mt], rloc, 64);
-      if (row < 0) continue;
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int col = n0 + nt * 32 + l32;
-        if (col < N) {
-          float v = acc[mt][nt][i];
-          if (bias) v += bias[col];
-          out[row * N + col] = from_f32<OutT>(v);
-        }
-      }
-    }
-  }
-}
+#include "sp_gather_gemm.h"
 
 // ---------------------------------------------------------------------------
 // weight gradient
@@ -387,27 +286,48 @@ static int pack_weight(const void* w, int w_dtype, const void* bias, int64_t K, 
   return SP_OK;
 }
 
+template <typename T, typename OutT, bool VEC, int RS>
+static void launch_one(dim3 grid, hipStream_t s, const T* A, const T* bt, const int32_t* pairs,
+                       const float* bias, OutT* o, GemmBufs nb, int64_t n_src, int64_t M, int N,
+                       int R, int Rp, int kv) {
+  gather_gemm<T, OutT, VEC, RS><<<grid, 256, 0, s>>>(A, bt, pairs, bias, o, nb, n_src, M, N, R,
+                                                    Rp, kv);
+}
+
+// The mask tables (pair_mask / mask_argsort) of the reference's masked path
+// are accepted but not needed: the kernel skips offsets that are empty for a
+// whole tile by itself and keeps rows in their natural order (better locality
+// for the gathers, the pair-table reads and the output writes).
 template <typename T, typename OutT>
 static int launch_gemm_typed(const T* A, int64_t n_src, const T* bt, const int32_t* pairs,
                              const int32_t* pm, const int32_t* ar, const float* bias, void* out,
                              int64_t M, int N, int R, int Rp, int kv, bool vec, hipStream_t s) {
+  (void)pm;
+  (void)ar;
   const int64_t gx = cdiv(M, 256);
   SP_CHECK_ARG(gx <= kMaxGridX, "gemm: too many rows");
+  // buffer instructions take 32-bit byte offsets
+  const int64_t lim = int64_t(kOob);
+  const int64_t a_bytes = n_src * R * int64_t(sizeof(T));
+  const int64_t bt_bytes = int64_t(kv) * Rp * N * int64_t(sizeof(T));
+  const int64_t p_bytes = int64_t(kv) * M * 4;
+  const int64_t o_bytes = M * N * int64_t(sizeof(OutT));
+  if (a_bytes >= lim || bt_bytes >= lim || p_bytes >= lim || o_bytes >= lim)
+    return set_error(SP_ERR_UNSUPPORTED,
+                     "gemm: a tensor exceeds 4 GiB (features %lld B, pairs %lld B, out %lld B)",
+                     (long long)a_bytes, (long long)p_bytes, (long long)o_bytes);
+  GemmBufs nb{uint32_t(a_bytes), uint32_t(bt_bytes), uint32_t(p_bytes), uint32_t(o_bytes)};
   const dim3 grid{unsigned(gx), unsigned(cdiv(N, 64)), 1u};
   OutT* o = static_cast<OutT*>(out);
-  const bool mask = pm && ar;
-  if (mask && vec)
-    gather_gemm<T, OutT, true, true><<<grid, 256, 0, s>>>(A, n_src, bt, pairs, pm, ar, bias, o, M,
-                                                         N, R, Rp, kv);
-  else if (mask)
-    gather_gemm<T, OutT, true, false><<<grid, 256, 0, s>>>(A, n_src, bt, pairs, pm, ar, bias, o, M,
-                                                          N, R, Rp, kv);
-  else if (vec)
-    gather_gemm<T, OutT, false, true><<<grid, 256, 0, s>>>(A, n_src, bt, pairs, pm, ar, bias, o, M,
-                                                          N, R, Rp, kv);
+  const int steps = Rp / Mfma<T>::KSTEP;
+  if (!vec)
+    launch_one<T, OutT, false, 1>(grid, s, A, bt, pairs, bias, o, nb, n_src, M, N, R, Rp, kv);
+  else if (steps % 4 == 0)
+    launch_one<T, OutT, true, 4>(grid, s, A, bt, pairs, bias, o, nb, n_src, M, N, R, Rp, kv);
+  else if (steps % 2 == 0)
+    launch_one<T, OutT, true, 2>(grid, s, A, bt, pairs, bias, o, nb, n_src, M, N, R, Rp, kv);
   else
-    gather_gemm<T, OutT, false, false><<<grid, 256, 0, s>>>(A, n_src, bt, pairs, pm, ar, bias, o,
-                                                           M, N, R, Rp, kv);
+    launch_one<T, OutT, true, 1>(grid, s, A, bt, pairs, bias, o, nb, n_src, M, N, R, Rp, kv);
   SP_LAUNCHED();
   return SP_OK;
 }
