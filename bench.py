@@ -105,7 +105,20 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device copy (reference point for the "
+                         "FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+
+        src = torch.ones(64 * 2 ** 20, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel() * 4}))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(the sparse-conv hot path shards by batch sample; see DESIGN.md)",
@@ -204,6 +217,12 @@ def main() -> int:
         torch.cuda.synchronize()
         kernel_ms = s.elapsed_time(e) / reps
 
+    # HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE runs,
+    # scaled by a 256 MiB copy (profiles/gather_gemm_traffic.json)
+    traffic = None
+    tfile = ROOT / "profiles" / "gather_gemm_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
     nbytes = gemm_bytes(N_VOXELS, N_VOXELS)
     flops = 2.0 * n_pairs * C_IN * C_OUT
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
@@ -245,7 +264,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "kernel": "gather_gemm<f16,f16,VEC,RS4>",
             "kernel_ms": round(kernel_ms, 5),
             "algorithmic_bytes": nbytes,

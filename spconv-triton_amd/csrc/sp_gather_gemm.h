@@ -2,8 +2,11 @@
 //
 //   out[m, n] = bias[n] + sum_k sum_r A[pairs[k, m], r] * Bt[k][n][r]
 //
-// One wave computes 64 consecutive output rows x 64 output columns as 2 x 2
-// tiles of v_mfma_f32_32x32x16_{f16,bf16} (v_mfma_f32_32x32x2f32 for fp32).
+// One wave computes 64 consecutive output rows x 64 output columns as 4 x 4
+// tiles of v_mfma_f32_16x16x32_{f16,bf16} (v_mfma_f32_16x16x4f32 for fp32);
+// the 16-row shape lets four lanes read one feature row's 64 contiguous bytes,
+// which halves the cache lines a gather instruction touches compared with the
+// 32-row shape.
 //
 // Memory access is built on raw buffer instructions: a load whose offset lies
 // past the buffer's size returns zeros and a store there is dropped, so a
@@ -87,12 +90,62 @@ struct GemmBufs {
   uint32_t a_bytes, bt_bytes, pairs_bytes, out_bytes;
 };
 
+// 16x16 MFMA shapes.  Lane l holds row (or column) l % 16 of the tile and the
+// 4 lane groups g = l / 16 hold consecutive slices of V reduction elements, so
+// one A-fragment load instruction reads 16 feature rows x 64 contiguous bytes.
+template <typename T>
+struct M16;
+
+template <>
+struct M16<_Float16> {
+  using frag = half8;
+  static constexpr int V = 8;
+  static constexpr int KSTEP = 32;
+  __device__ static __forceinline__ void mma(const frag& a, const frag& b, float4v& c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct M16<__bf16> {
+  using frag = bf16x8;
+  static constexpr int V = 8;
+  static constexpr int KSTEP = 32;
+  __device__ static __forceinline__ void mma(const frag& a, const frag& b, float4v& c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct M16<float> {
+  using frag = float4v;
+  static constexpr int V = 4;
+  static constexpr int KSTEP = 16;
+  __device__ static __forceinline__ void mma(const frag& a, const frag& b, float4v& c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[2], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[3], c, 0, 0, 0);
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ typename M16<T>::frag buf_frag16(__amdgpu_buffer_rsrc_t r,
+                                                            uint32_t off) {
+  return __builtin_bit_cast(typename M16<T>::frag,
+                            __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// One wave computes 64 rows x 64 columns as 4 x 4 tiles of 16 x 16.  RS = MFMA
+// K-steps per pipeline item (RS * KSTEP reduction indices).  The reduction
+// index of (step s, lane group g, element e) is s * KSTEP + g * V + e, for A
+// and B alike.
 template <typename T, typename OutT, bool VEC, int RS>
 __global__ __launch_bounds__(256) void gather_gemm(
     const T* __restrict__ A, const T* __restrict__ Bt, const int32_t* __restrict__ pairs,
     const float* __restrict__ bias, OutT* __restrict__ out, GemmBufs nb, int64_t n_src,
     int64_t M, int N, int R, int Rp, int kv) {
-  using MF = Mfma<T>;
+  using MF = M16<T>;
   using frag = typename MF::frag;
   constexpr int V = MF::V;
   constexpr int KSTEP = MF::KSTEP;
@@ -102,7 +155,7 @@ __global__ __launch_bounds__(256) void gather_gemm(
   __shared__ int32_t s_k[4][kStageOffsets];
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int h = lane >> 5, l32 = lane & 31;
+  const int g = lane >> 4, l16 = lane & 15;
   const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
   const int64_t slot0 = (tile * 4 + wave) * 64;
   const int n0 = blockIdx.y * 64;
@@ -114,20 +167,24 @@ __global__ __launch_bounds__(256) void gather_gemm(
   const __amdgpu_buffer_rsrc_t rp = make_rsrc(pairs, nb.pairs_bytes);
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(out, nb.out_bytes);
 
-  floatx16 acc[2][2];
+  float4v acc[4][4];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.f;
+      for (int i = 0; i < 4; ++i) acc[mt][nt][i] = 0.f;
 
   const uint32_t bk_bytes = uint32_t(Rp / V) * uint32_t(N) * V * ES;  // one offset of Bt
   const uint32_t row_bytes = uint32_t(R) * ES;
   const int nrc = Rp / RCH;  // reduction chunks per offset
   int32_t* src_tab = &s_src[wave][0][0];
-  // per-lane B column byte offset (the lane's column of an (offset, r/V) slab)
-  const int col0 = n0 + l32, col1 = n0 + 32 + l32;
+  uint32_t bcol[4];  // byte offset of this lane's B column inside an (offset, r/V) slab
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    const int col = n0 + nt * 16 + l16;
+    bcol[nt] = col < N ? uint32_t(col) * V * ES : kOob;
+  }
 
   for (int kc = 0; kc < kv; kc += kStageOffsets) {
     const int kn = kv - kc < kStageOffsets ? kv - kc : kStageOffsets;
@@ -156,25 +213,25 @@ __global__ __launch_bounds__(256) void gather_gemm(
 
     // ---- pipelined gather + MFMA over (offset, reduction chunk) items
     const int nitems = nact * nrc;
-    auto load_item = [&](int it, frag (&a)[2][RS], frag (&b)[2][RS]) {
+    auto load_item = [&](int it, frag (&a)[4][RS], frag (&b)[4][RS]) {
       const int si = it / nrc;
       const int rc = it - si * nrc;
       const uint32_t kb = uint32_t(s_k[wave][si]) * bk_bytes;
-      uint32_t abase[2];
+      uint32_t abase[4];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const int32_t s = src_tab[si * 64 + mt * 32 + l32];
+      for (int mt = 0; mt < 4; ++mt) {
+        const int32_t s = src_tab[si * 64 + mt * 16 + l16];
         abase[mt] = s >= 0 ? uint32_t(s) * row_bytes : kOob;
       }
 #pragma unroll
       for (int st = 0; st < RS; ++st) {
-        const int rr = rc * RCH + st * KSTEP + h * V;
+        const int rr = rc * RCH + st * KSTEP + g * V;
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt) {
+        for (int mt = 0; mt < 4; ++mt) {
           if (VEC) {
             const uint32_t off = (abase[mt] != kOob && rr < R) ? abase[mt] + uint32_t(rr) * ES
                                                                : kOob;
-            a[mt][st] = buf_frag<T>(ra, off);
+            a[mt][st] = buf_frag16<T>(ra, off);
           } else {
 #pragma unroll
             for (int e = 0; e < V; ++e) {
@@ -186,19 +243,20 @@ __global__ __launch_bounds__(256) void gather_gemm(
           }
         }
         const uint32_t slab = kb + uint32_t(rr / V) * uint32_t(N) * V * ES;
-        b[0][st] = buf_frag<T>(rb, col0 < N ? slab + uint32_t(col0) * V * ES : kOob);
-        b[1][st] = buf_frag<T>(rb, col1 < N ? slab + uint32_t(col1) * V * ES : kOob);
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          b[nt][st] = buf_frag16<T>(rb, bcol[nt] != kOob ? slab + bcol[nt] : kOob);
       }
     };
-    auto mma_item = [&](const frag (&a)[2][RS], const frag (&b)[2][RS]) {
+    auto mma_item = [&](const frag (&a)[4][RS], const frag (&b)[4][RS]) {
 #pragma unroll
       for (int st = 0; st < RS; ++st)
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+        for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt) MF::mma(a[mt][st], b[nt][st], acc[mt][nt]);
+          for (int nt = 0; nt < 4; ++nt) MF::mma(a[mt][st], b[nt][st], acc[mt][nt]);
     };
-    frag a0[2][RS], b0[2][RS], a1[2][RS], b1[2][RS];
+    frag a0[4][RS], b0[4][RS], a1[4][RS], b1[4][RS];
     if (nitems > 0) load_item(0, a0, b0);
     for (int it = 0; it < nitems; it += 2) {
       if (it + 1 < nitems) load_item(it + 1, a1, b1);
@@ -211,26 +269,21 @@ __global__ __launch_bounds__(256) void gather_gemm(
     __syncthreads();  // the next chunk overwrites the staged sources
   }
 
-  // ---- epilogue: lane l holds column l%32 of rows 8*(i/4) + 4*h + (i%4);
+  // ---- epilogue: lane l holds column l%16 of rows 4*(l/16) + i of each tile;
   // rows past M fall outside the output buffer and their stores are dropped
-  float bv[2];
 #pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int col = n0 + nt * 32 + l32;
-    bv[nt] = (bias && col < N) ? bias[col] : 0.f;
-  }
+  for (int nt = 0; nt < 4; ++nt) {
+    const int col = n0 + nt * 16 + l16;
+    const float bv = (bias && col < N) ? bias[col] : 0.f;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < 4; ++mt) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int64_t row = slot0 + mt * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int col = n0 + nt * 32 + l32;
+      for (int i = 0; i < 4; ++i) {
+        const int64_t row = slot0 + mt * 16 + g * 4 + i;
         const uint32_t off = (row < M && col < N)
                                  ? uint32_t((row * N + col) * int64_t(sizeof(OutT)))
                                  : kOob;
-        buf_store<OutT>(from_f32<OutT>(acc[mt][nt][i] + bv[nt]), ro, off);
+        buf_store<OutT>(from_f32<OutT>(acc[mt][nt][i] + bv), ro, off);
       }
     }
   }

@@ -245,8 +245,8 @@ static Packed packed_layout(int64_t K, int64_t kv, int64_t C, int dtype, int tra
   Packed p;
   p.N = int(transpose ? C : K);
   p.R = int(transpose ? K : C);
-  // the reduction runs in MFMA steps of 2 * V (two lane halves of V each)
-  p.Rp = int(padded(p.R, 2 * vec_of(dtype)));
+  // the reduction runs in MFMA steps of 4 * V (four lane groups of V each)
+  p.Rp = int(padded(p.R, 4 * vec_of(dtype)));
   p.bt_bytes = size_t(kv) * size_t(p.Rp) * size_t(p.N) * size_t(elem_size(dtype));
   p.bias_off = align_up(p.bt_bytes, 256);
   p.total = p.bias_off + align_up(size_t(p.N) * sizeof(float), 256);
@@ -319,7 +319,7 @@ static int launch_gemm_typed(const T* A, int64_t n_src, const T* bt, const int32
   GemmBufs nb{uint32_t(a_bytes), uint32_t(bt_bytes), uint32_t(p_bytes), uint32_t(o_bytes)};
   const dim3 grid{unsigned(gx), unsigned(cdiv(N, 64)), 1u};
   OutT* o = static_cast<OutT*>(out);
-  const int steps = Rp / Mfma<T>::KSTEP;
+  const int steps = Rp / M16<T>::KSTEP;
   if (!vec)
     launch_one<T, OutT, false, 1>(grid, s, A, bt, pairs, bias, o, nb, n_src, M, N, R, Rp, kv);
   else if (steps % 4 == 0)
