@@ -1,45 +1,71 @@
-// Forward / input-gradient gather-GEMM kernel (included by sp_gemm.hip).
+// Forward / input-gradient gather-GEMM kernels (included by sp_gemm.hip).
 //
 //   out[m, n] = bias[n] + sum_k sum_r A[pairs[k, m], r] * Bt[k][n][r]
 //
-// One wave computes 64 consecutive output rows x 64 output columns as 4 x 4
-// tiles of v_mfma_f32_16x16x32_{f16,bf16} (v_mfma_f32_16x16x4f32 for fp32);
-// the 16-row shape lets four lanes read one feature row's 64 contiguous bytes,
-// which halves the cache lines a gather instruction touches compared with the
-// 32-row shape.
+// A workgroup owns kTileRows = 256 consecutive output rows x 64 output columns;
+// each of its 4 waves computes 64 rows x 64 columns as 2 x 2 tiles of
+// v_mfma_f32_32x32x16_{f16,bf16} (4 x v_mfma_f32_32x32x2f32 for fp32, the
+// Mfma<> traits).  Measured on MI355X, one 32x32x16 issues every ~38.5 clocks
+// per SIMD whether one or two waves share the SIMD (2.1 PFLOP/s), while
+// 16x16x32 needs two interleaved waves to get near that (31 clocks per half
+// the work for a lone wave).  One "item" is one kernel offset for one chunk
+// of 64 bytes of the reduction dimension (32 f16/bf16 or 16 f32): 8 MFMAs per
+// wave fed by 4 A fragments (gathered rows) and 4 B fragments (weights).
 //
-// Memory access is built on raw buffer instructions: a load whose offset lies
-// past the buffer's size returns zeros and a store there is dropped, so a
-// missing neighbour (pair index -1) is just an out-of-range offset -- no
-// branch per load.  Branch-free loads also let the compiler count outstanding
-// loads exactly, which the software pipeline below depends on.
+// Two kernels:
+//  * gather_gemm_staged (with a gather plan, sp_plan.h).  Measured on MI355X,
+//    LDS delivers ~228 B/clk per CU against ~60 B/clk for L1 hits, so both
+//    operands come from LDS:
+//      - A: for each chunk the workgroup copies the tile's distinct source
+//        rows (~765 for 256 rows of a surface cloud, against ~2600 pairs)
+//        into LDS with coalesced 16-byte loads, four lanes per row; the next
+//        chunk's rows are loaded into registers while the current one is
+//        multiplied.  Fragments are read at the LDS addresses the plan holds
+//        for every (item, row).
+//      - B: the four waves share the tile's item list, and each item's 4 KiB
+//        weight slab is loaded once per workgroup (16 bytes per thread) into a
+//        3-slot LDS ring, one barrier per item.
+//    Tiles whose distinct rows do not fit in LDS (the plan's overflow list)
+//    are left to the direct kernel.
+//  * gather_gemm_direct: fragments are gathered straight from global memory
+//    (A) and B is read through L1 by every wave.  It runs every tile of an
+//    unplanned call, or only the overflow tiles of a planned one, and builds
+//    its per-wave item tables from the pair table itself.
 //
-// Per chunk of up to 32 kernel offsets the wave stages the source row of each
-// (offset, row) in LDS, with all pair-table loads in flight at once, and keeps
-// only the offsets that have a valid source somewhere in its 64 rows (ballot).
-// It then pipelines over (offset, reduction chunk) items: the A (gathered
-// feature rows) and B (packed weights) fragments of item i+1 are loaded while
-// the MFMAs of item i run.  Rows keep their natural order: the [kv, M] pair
-// table is read with coalesced 256-byte accesses and output rows are
-// contiguous.  Every row's sum runs over its offsets in ascending order for any
-// tiling, so skipped offsets and tile composition never change a result bit.
-// Included inside namespace sp, after the Mfma<> traits and from_f32<>.
+// Both pipelines keep per-item work to loads and MFMAs: B offsets and A
+// addresses are precomputed per item, and the item lists end with kPad
+// padding items (zero row, out-of-range B), so the loops run in whole groups of
+// 3 items and read ahead without per-item conditions.  Padding items multiply
+// zeros, which leaves every sum unchanged.  Raw buffer instructions make global
+// loads branch-free (an offset past the buffer's size reads zeros, a store
+// there is dropped), and sched_barrier keeps loads issued ahead of the MFMAs
+// that consume them, so the compiler's load counters stay exact.
+//
+// Fragment layouts (32 x 32 MFMA, lane l, h = l / 32): A and B fragments hold
+// row (column) l % 32 of the tile and 16-byte piece 2 * ks + h of the 64-byte
+// chunk, ks = 0, 1 being the MFMA K-step within the item; the accumulator
+// element i of lane l is row 8 * (i / 4) + 4 * h + i % 4, column l % 32.
+//
+// Summation order.  Offsets are taken in groups of up to 64 (one group when
+// kv <= 64); within a group the chunks are the outer loop and the offsets,
+// ascending, the inner one.  Offsets without any pair in the wave's (direct)
+// or the tile's (staged) rows are skipped; their terms are exactly zero, so a
+// row's result does not depend on the tile it falls in or on the kernel.
+// Included inside namespace sp, after sp_plan.h, the Mfma<> traits and
+// from_f32<>.
 #pragma once
 
-constexpr int kStageOffsets = 32;  // kernel offsets staged in LDS at once
-constexpr uint32_t kOob = 0xFFFFFFF0u;  // byte offset past every buffer (loads give 0)
+constexpr uint32_t kOob = 0xFFFFFFF0u;     // byte offset past every buffer (loads give 0)
+constexpr uint32_t kBOob = 0x80000000u;    // B offset of padding items
+constexpr uint32_t kColOob = 0x40000000u;  // B column offset of columns >= N
+constexpr uint32_t kMaxBtBytes = 0x40000000u;  // packed weights must stay below (host check)
+constexpr int kGroupOffsets = 64;          // kernel offsets per group (direct kernel)
+constexpr uint32_t kSlabBytes = 4096;      // B of one item: 4 pieces x 64 columns x 16 B
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   // word 3 = 0x00020000: 32-bit data format, the raw-buffer setting for gfx9 parts
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, int(bytes),
                                            0x00020000);
-}
-
-template <typename T>
-__device__ __forceinline__ typename Mfma<T>::frag buf_frag(__amdgpu_buffer_rsrc_t r,
-                                                           uint32_t off) {
-  return __builtin_bit_cast(typename Mfma<T>::frag,
-                            __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
 template <typename T>
@@ -85,206 +111,513 @@ __device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t nb) {
   return x < r ? x * (q + 1) + local : r * (q + 1) + (x - r) * q + local;
 }
 
+// LDS writes of this wave are complete, then the workgroup barrier.  Written
+// as one asm statement with a memory clobber: the compiler neither moves LDS
+// accesses across it nor adds waits for outstanding global loads (which the
+// B and A pipelines keep in flight across barriers).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Byte sizes of the buffers a launch touches; the host checks they fit in 32 bits.
 struct GemmBufs {
   uint32_t a_bytes, bt_bytes, pairs_bytes, out_bytes;
 };
 
-// 16x16 MFMA shapes.  Lane l holds row (or column) l % 16 of the tile and the
-// 4 lane groups g = l / 16 hold consecutive slices of V reduction elements, so
-// one A-fragment load instruction reads 16 feature rows x 64 contiguous bytes.
 template <typename T>
-struct M16;
-
-template <>
-struct M16<_Float16> {
-  using frag = half8;
-  static constexpr int V = 8;
-  static constexpr int KSTEP = 32;
-  __device__ static __forceinline__ void mma(const frag& a, const frag& b, float4v& c) {
-    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
-
-template <>
-struct M16<__bf16> {
-  using frag = bf16x8;
-  static constexpr int V = 8;
-  static constexpr int KSTEP = 32;
-  __device__ static __forceinline__ void mma(const frag& a, const frag& b, float4v& c) {
-    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-};
-
-template <>
-struct M16<float> {
-  using frag = float4v;
-  static constexpr int V = 4;
-  static constexpr int KSTEP = 16;
-  __device__ static __forceinline__ void mma(const frag& a, const frag& b, float4v& c) {
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[1], c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[2], c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[3], c, 0, 0, 0);
-  }
-};
-
-template <typename T>
-__device__ __forceinline__ typename M16<T>::frag buf_frag16(__amdgpu_buffer_rsrc_t r,
-                                                            uint32_t off) {
-  return __builtin_bit_cast(typename M16<T>::frag,
+__device__ __forceinline__ typename Mfma<T>::frag buf_frag(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(typename Mfma<T>::frag,
                             __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
-// One wave computes 64 rows x 64 columns as 4 x 4 tiles of 16 x 16.  RS = MFMA
-// K-steps per pipeline item (RS * KSTEP reduction indices).  The reduction
-// index of (step s, lane group g, element e) is s * KSTEP + g * V + e, for A
-// and B alike.
-template <typename T, typename OutT, bool VEC, int RS>
-__global__ __launch_bounds__(256) void gather_gemm(
+// V elements of one row starting at element e0 (zeros past R), one load per
+// element: the path for rows whose length is not a multiple of V.
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::frag buf_frag_elems(__amdgpu_buffer_rsrc_t r,
+                                                                 uint32_t row_off, int e0, int R) {
+  typename Mfma<T>::frag f;
+#pragma unroll
+  for (int e = 0; e < Mfma<T>::V; ++e) {
+    const uint32_t off =
+        (row_off != kOob && e0 + e < R) ? row_off + uint32_t(e0 + e) * uint32_t(sizeof(T)) : kOob;
+    f[e] = buf_elem<T>(r, off);
+  }
+  return f;
+}
+
+// One item: fragments [ks][mt] (A) and [ks][nt] (B), K-steps ascending.
+template <typename T>
+__device__ __forceinline__ void mma_item(const typename Mfma<T>::frag (&a)[2][2],
+                                         const typename Mfma<T>::frag (&b)[2][2],
+                                         floatx16 (&acc)[2][2]) {
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) Mfma<T>::mma(a[ks][mt], b[ks][nt], acc[mt][nt]);
+}
+
+__device__ __forceinline__ void zero_acc(floatx16 (&acc)[2][2]) {
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.f;
+}
+
+// Epilogue staging: each wave's 64 x 64 output tile, rows padded by 16 bytes.
+__host__ __device__ constexpr uint32_t epi_pitch(uint32_t out_size) { return 64u * out_size + 16u; }
+__host__ __device__ constexpr uint32_t epi_bytes(uint32_t out_size) {
+  return 4u * 64u * epi_pitch(out_size);
+}
+
+// Writes the wave's 64 x 64 tile (plus bias).  When a row's 64 columns split
+// into whole 16-byte pieces, the tile goes through LDS (`stage`, this wave's
+// 64 * epi_pitch bytes, free once the caller has passed a barrier) and is
+// stored as whole rows, otherwise element by element.  Rows past M fall
+// outside the output buffer and their stores are dropped.
+template <typename OutT>
+__device__ __forceinline__ void store_tile(const floatx16 (&acc)[2][2], const float* bias,
+                                           __amdgpu_buffer_rsrc_t ro, unsigned char* stage,
+                                           int64_t slot0, int n0, int64_t M, int N, int lane) {
+  constexpr uint32_t OS = sizeof(OutT);
+  constexpr int kPer16 = int(16 / OS);  // output elements per 16-byte piece
+  const int h = lane >> 5, l32 = lane & 31;
+  if (N % kPer16 == 0) {
+    constexpr uint32_t pitch = epi_pitch(OS);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int col = n0 + nt * 32 + l32;
+      const float bv = (bias && col < N) ? bias[col] : 0.f;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          *reinterpret_cast<OutT*>(stage +
+                                   uint32_t(mt * 32 + 8 * (i / 4) + 4 * h + (i % 4)) * pitch +
+                                   uint32_t(nt * 32 + l32) * OS) =
+              from_f32<OutT>(acc[mt][nt][i] + bv);
+    }
+    // (each wave reads back only its own rows: no barrier needed)
+    constexpr int kPieces = 64 / kPer16;        // 16-byte pieces per row of 64 columns
+    constexpr int kRowsPerPass = 64 / kPieces;  // rows one instruction covers
+    const int pc = lane % kPieces, pr = lane / kPieces;
+    const int col = n0 + pc * kPer16;
+#pragma unroll
+    for (int j = 0; j < 64 / kRowsPerPass; ++j) {
+      const int r = pr + j * kRowsPerPass;
+      const uint4 v =
+          *reinterpret_cast<const uint4*>(stage + uint32_t(r) * pitch + uint32_t(pc) * 16u);
+      const int64_t row = slot0 + r;
+      const uint32_t off = (row < M && col < N) ? uint32_t((row * N + col) * int64_t(OS)) : kOob;
+      __builtin_amdgcn_raw_buffer_store_b128(
+          __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, v), ro, off, 0, 0);
+    }
+    return;
+  }
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int col = n0 + nt * 32 + l32;
+    const float bv = (bias && col < N) ? bias[col] : 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int64_t row = slot0 + mt * 32 + 8 * (i / 4) + 4 * h + (i % 4);
+        const uint32_t off =
+            (row < M && col < N) ? uint32_t((row * N + col) * int64_t(OS)) : kOob;
+        buf_store<OutT>(from_f32<OutT>(acc[mt][nt][i] + bv), ro, off);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// direct kernel
+// ---------------------------------------------------------------------------
+
+// Dynamic LDS of the direct kernel: per wave E item entries; the epilogue
+// tiles overlap the tables (used after the last item).
+struct DirectLds {
+  uint32_t kb_off, src_off, total;
+};
+
+__host__ __device__ inline DirectLds direct_lds(int E, uint32_t out_size) {
+  DirectLds l;
+  l.kb_off = 0;                                          // uint32 B offsets [4][E]
+  l.src_off = (16u * uint32_t(E) + 255u) / 256u * 256u;  // int32 source rows [4][E][32][2]
+  l.total = l.src_off + uint32_t(E) * 1024u;
+  if (l.total < l.src_off + epi_bytes(out_size)) l.total = l.src_off + epi_bytes(out_size);
+  return l;
+}
+
+// All tiles (plan.count == nullptr) or, with a plan, the overflow tiles only,
+// one workgroup per list entry.
+template <typename T, typename OutT, bool VEC>
+__global__ __launch_bounds__(256, 2) void gather_gemm_direct(
     const T* __restrict__ A, const T* __restrict__ Bt, const int32_t* __restrict__ pairs,
-    const float* __restrict__ bias, OutT* __restrict__ out, GemmBufs nb, int64_t n_src,
-    int64_t M, int N, int R, int Rp, int kv) {
-  using MF = M16<T>;
-  using frag = typename MF::frag;
-  constexpr int V = MF::V;
-  constexpr int KSTEP = MF::KSTEP;
-  constexpr int RCH = RS * KSTEP;
+    PlanDev plan, const float* __restrict__ bias, OutT* __restrict__ out, GemmBufs nb,
+    int64_t n_src, int64_t M, int N, int R, int Rp, int kv) {
+  using frag = typename Mfma<T>::frag;
+  constexpr int V = Mfma<T>::V;
   constexpr uint32_t ES = sizeof(T);
-  __shared__ int32_t s_src[4][kStageOffsets][64];
-  __shared__ int32_t s_k[4][kStageOffsets];
+  constexpr int kChunk = kChunkBytes / int(ES);  // reduction elements per item
+  extern __shared__ __align__(16) unsigned char smem[];
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int g = lane >> 4, l16 = lane & 15;
-  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
-  const int64_t slot0 = (tile * 4 + wave) * 64;
+  const int h = lane >> 5, l32 = lane & 31;
+  int64_t tile;
+  if (plan.count != nullptr) {
+    if (int(blockIdx.x) >= *plan.n_overflow) return;
+    tile = plan.overflow[blockIdx.x];
+    if (tile < 0 || tile * kTileRows >= M) return;
+  } else {
+    tile = xcd_tile(blockIdx.x, gridDim.x);
+  }
+  const int64_t slot0 = tile * kTileRows + wave * 64;
   const int n0 = blockIdx.y * 64;
   const int64_t my_row = slot0 + lane;
   const bool row_ok = my_row < M;
 
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, nb.a_bytes);
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bt, nb.bt_bytes);
-  const __amdgpu_buffer_rsrc_t rp = make_rsrc(pairs, nb.pairs_bytes);
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(out, nb.out_bytes);
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(pairs, nb.pairs_bytes);
 
-  float4v acc[4][4];
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[mt][nt][i] = 0.f;
+  const int G = kv < kGroupOffsets ? kv : kGroupOffsets;
+  const int E = G + kPad;
+  const DirectLds L = direct_lds(E, uint32_t(sizeof(OutT)));
+  uint32_t* s_kb = reinterpret_cast<uint32_t*>(smem + L.kb_off) + wave * E;
+  int32_t* s_src = reinterpret_cast<int32_t*>(smem + L.src_off) + wave * E * 64;
 
-  const uint32_t bk_bytes = uint32_t(Rp / V) * uint32_t(N) * V * ES;  // one offset of Bt
   const uint32_t row_bytes = uint32_t(R) * ES;
-  const int nrc = Rp / RCH;  // reduction chunks per offset
-  int32_t* src_tab = &s_src[wave][0][0];
-  uint32_t bcol[4];  // byte offset of this lane's B column inside an (offset, r/V) slab
+  const uint32_t slab_bytes = uint32_t(N) * V * ES;        // one (offset, r / V) slab of Bt
+  const uint32_t k_bytes = uint32_t(Rp / V) * slab_bytes;  // one offset of Bt
+  const int nrc = Rp / kChunk;                             // chunks per offset
+  uint32_t bcol[2];  // byte offset of this lane's B column inside a slab
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const int col = n0 + nt * 16 + l16;
-    bcol[nt] = col < N ? uint32_t(col) * V * ES : kOob;
+  for (int nt = 0; nt < 2; ++nt) {
+    const int col = n0 + nt * 32 + l32;
+    bcol[nt] = col < N ? uint32_t(col) * V * ES : kColOob;
   }
 
-  for (int kc = 0; kc < kv; kc += kStageOffsets) {
-    const int kn = kv - kc < kStageOffsets ? kv - kc : kStageOffsets;
-    // ---- stage the source rows of the offsets that are live in this tile
+  floatx16 acc[2][2];
+  zero_acc(acc);
+  for (int kc = 0; kc < kv; kc += G) {
+    const int kn = kv - kc < G ? kv - kc : G;
+    __syncthreads();  // the previous group's tables are no longer read
+    // ---- per-wave tables of the offsets with a pair in this wave's 64 rows
     int nact = 0;
-    for (int u0 = 0; u0 < kn; u0 += 8) {
-      int32_t v[8];
+    constexpr int kTabBatch = 16;  // table loads in flight per lane
+    for (int u0 = 0; u0 < kn; u0 += kTabBatch) {
+      int32_t v[kTabBatch];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const uint32_t off = row_ok && u0 + u < kn
-                                 ? uint32_t((int64_t(kc + u0 + u) * M + my_row) * 4)
-                                 : kOob;
-        v[u] = int32_t(__builtin_amdgcn_raw_buffer_load_b32(rp, off, 0, 0));
+      for (int u = 0; u < kTabBatch; ++u) {
+        const bool in = row_ok && u0 + u < kn;
+        const int64_t e = int64_t(kc + u0 + u) * M + my_row;
+        v[u] = int32_t(__builtin_amdgcn_raw_buffer_load_b32(rp, in ? uint32_t(e * 4) : kOob, 0, 0));
       }
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < kTabBatch; ++u) {
         const bool ok = row_ok && u0 + u < kn && v[u] >= 0 && v[u] < n_src;
-        if (__ballot(ok)) {  // wave-uniform
-          src_tab[nact * 64 + lane] = ok ? v[u] : -1;
-          if (lane == 0) s_k[wave][nact] = kc + u0 + u;
+        if (u0 + u < kn && __ballot(ok)) {  // wave-uniform
+          s_src[(nact * 32 + l32) * 2 + h] = ok ? v[u] : -1;  // [item][l32][mt], mt = lane / 32
+          if (lane == 0) s_kb[nact] = uint32_t(kc + u0 + u) * k_bytes;
           ++nact;
         }
       }
     }
-    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < kPad; ++q) {  // padding items: no source row, out-of-range B
+      s_src[((nact + q) * 32 + l32) * 2 + h] = -1;
+      if (lane == 0) s_kb[nact + q] = kBOob;
+    }
 
-    // ---- pipelined gather + MFMA over (offset, reduction chunk) items
-    const int nitems = nact * nrc;
-    auto load_item = [&](int it, frag (&a)[4][RS], frag (&b)[4][RS]) {
-      const int si = it / nrc;
-      const int rc = it - si * nrc;
-      const uint32_t kb = uint32_t(s_k[wave][si]) * bk_bytes;
-      uint32_t abase[4];
+    for (int rc = 0; rc < nrc; ++rc) {
+      // Step `it`: the A loads of item it+1 and the table entries of item it+2,
+      // then the MFMAs of item it, then the B loads of item it+2.
+      uint32_t bl[2][2];  // this lane's B offsets inside an offset's slabs
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt) {
-        const int32_t s = src_tab[si * 64 + mt * 16 + l16];
-        abase[mt] = s >= 0 ? uint32_t(s) * row_bytes : kOob;
-      }
+      for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int st = 0; st < RS; ++st) {
-        const int rr = rc * RCH + st * KSTEP + g * V;
+        for (int nt = 0; nt < 2; ++nt)
+          bl[ks][nt] = bcol[nt] + uint32_t(rc * 4 + ks * 2 + h) * slab_bytes;
+      auto entry = [&](int it) -> int2 {
+        return *reinterpret_cast<const int2*>(s_src + (it * 32 + l32) * 2);
+      };
+      auto load_b = [&](uint32_t kb, frag (&b)[2][2]) {
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt) {
-          if (VEC) {
-            const uint32_t off = (abase[mt] != kOob && rr < R) ? abase[mt] + uint32_t(rr) * ES
-                                                               : kOob;
-            a[mt][st] = buf_frag16<T>(ra, off);
-          } else {
+        for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-            for (int e = 0; e < V; ++e) {
-              const uint32_t off = (abase[mt] != kOob && rr + e < R)
-                                       ? abase[mt] + uint32_t(rr + e) * ES
-                                       : kOob;
-              a[mt][st][e] = buf_elem<T>(ra, off);
-            }
+          for (int nt = 0; nt < 2; ++nt) b[ks][nt] = buf_frag<T>(rb, kb + bl[ks][nt]);
+      };
+      auto load_a = [&](const int2& e, frag (&a)[2][2]) {
+        const int32_t s2[2] = {e.x, e.y};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const int e0 = rc * kChunk + (ks * 2 + h) * V;  // first element of this lane's piece
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt) {
+            const uint32_t base = s2[mt] >= 0 ? uint32_t(s2[mt]) * row_bytes : kOob;
+            if (VEC)
+              a[ks][mt] =
+                  buf_frag<T>(ra, (base != kOob && e0 < R) ? base + uint32_t(e0) * ES : kOob);
+            else
+              a[ks][mt] = buf_frag_elems<T>(ra, base, e0, R);
           }
         }
-        const uint32_t slab = kb + uint32_t(rr / V) * uint32_t(N) * V * ES;
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt)
-          b[nt][st] = buf_frag16<T>(rb, bcol[nt] != kOob ? slab + bcol[nt] : kOob);
+      };
+      frag b0[2][2], b1[2][2], b2[2][2], a0[2][2], a1[2][2], a2[2][2];
+      int2 e_next;
+      {
+        const uint32_t k0 = s_kb[0], k1 = s_kb[1];
+        const int2 e0 = entry(0);
+        e_next = entry(1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(k0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(k1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_a(e0, a0);
+        __builtin_amdgcn_sched_barrier(0);
       }
-    };
-    auto mma_item = [&](const frag (&a)[4][RS], const frag (&b)[4][RS]) {
-#pragma unroll
-      for (int st = 0; st < RS; ++st)
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-          for (int nt = 0; nt < 4; ++nt) MF::mma(a[mt][st], b[nt][st], acc[mt][nt]);
-    };
-    frag a0[4][RS], b0[4][RS], a1[4][RS], b1[4][RS];
-    if (nitems > 0) load_item(0, a0, b0);
-    for (int it = 0; it < nitems; it += 2) {
-      if (it + 1 < nitems) load_item(it + 1, a1, b1);
-      mma_item(a0, b0);
-      if (it + 1 < nitems) {
-        if (it + 2 < nitems) load_item(it + 2, a0, b0);
-        mma_item(a1, b1);
+      auto step = [&](int it, frag (&bc)[2][2], frag (&bn)[2][2], frag (&ac)[2][2],
+                      frag (&an)[2][2]) {
+        load_a(e_next, an);
+        const uint32_t k2 = s_kb[it + 2];
+        const int2 e2 = entry(it + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_item<T>(ac, bc, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(k2, bn);
+        __builtin_amdgcn_sched_barrier(0);
+        e_next = e2;
+      };
+      step(0, b0, b2, a0, a1);
+      step(1, b1, b0, a1, a2);
+      step(2, b2, b1, a2, a0);
+      for (int it = 3; it < nact; it += 3) {  // reads entries up to max(nact + 3, 4) < nact + kPad
+        step(it, b0, b2, a0, a1);
+        step(it + 1, b1, b0, a1, a2);
+        step(it + 2, b2, b1, a2, a0);
       }
     }
-    __syncthreads();  // the next chunk overwrites the staged sources
   }
+  __syncthreads();  // the tables are free for the epilogue
+  store_tile<OutT>(acc, bias, ro, smem + L.src_off + uint32_t(wave) * 64u * epi_pitch(sizeof(OutT)),
+                   slot0, n0, M, N, lane);
+}
 
-  // ---- epilogue: lane l holds column l%16 of rows 4*(l/16) + i of each tile;
-  // rows past M fall outside the output buffer and their stores are dropped
+// ---------------------------------------------------------------------------
+// staged kernel
+// ---------------------------------------------------------------------------
+
+// Dynamic LDS of the staged kernel: B offsets of the tile's items, the byte
+// offsets of the tile's distinct rows in A, the staged rows (kLdsRows chunks)
+// and the B ring (3 slabs); the epilogue tiles overlap the staged rows and the
+// ring.
+struct StagedLds {
+  uint32_t kb_off, rowoff_off, rows_off, ring_off, total;
+};
+
+__host__ __device__ inline StagedLds staged_lds(int E, uint32_t out_size) {
+  StagedLds l;
+  l.kb_off = 0;
+  l.rowoff_off = (4u * uint32_t(E) + 255u) / 256u * 256u;
+  l.rows_off = l.rowoff_off + uint32_t(kLdsRows) * 4u;
+  l.ring_off = l.rows_off + uint32_t(kLdsRows * kChunkBytes);
+  l.total = l.ring_off + 3u * kSlabBytes;
+  if (l.total < l.rows_off + epi_bytes(out_size)) l.total = l.rows_off + epi_bytes(out_size);
+  return l;
+}
+
+// Tiles of the plan that fit in LDS (plan required, kv <= kPlanMaxKv).
+template <typename T, typename OutT, bool VEC>
+__global__ __launch_bounds__(256, 2) void gather_gemm_staged(
+    const T* __restrict__ A, const T* __restrict__ Bt, PlanDev plan,
+    const float* __restrict__ bias, OutT* __restrict__ out, GemmBufs nb, int64_t M, int N,
+    int R, int Rp, int kv) {
+  using frag = typename Mfma<T>::frag;
+  constexpr int V = Mfma<T>::V;
+  constexpr uint32_t ES = sizeof(T);
+  constexpr int kChunk = kChunkBytes / int(ES);  // reduction elements per item
+  constexpr int kRowsPerLane = kLdsRows / 64;    // staged rows copied per thread and chunk
+  static_assert(V * ES == 16, "fragments and B slab pieces are 16 bytes");
+  static_assert(kLdsRows % 64 == 0, "rows are copied 64 per workgroup pass");
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int64_t slot0 = tile * kTileRows + wave * 64;
+  const int n0 = blockIdx.y * 64;
+
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, nb.a_bytes);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bt, nb.bt_bytes);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(out, nb.out_bytes);
+
+  const int E = kv + kPad;
+  const StagedLds L = staged_lds(E, uint32_t(sizeof(OutT)));
+  uint32_t* s_kb = reinterpret_cast<uint32_t*>(smem + L.kb_off);
+  unsigned char* rows_lds = smem + L.rows_off;
+  unsigned char* ring = smem + L.ring_off;
+
+  const uint32_t row_bytes = uint32_t(R) * ES;
+  const uint32_t slab_bytes = uint32_t(N) * V * ES;        // one (offset, r / V) slab of Bt
+  const uint32_t k_bytes = uint32_t(Rp / V) * slab_bytes;  // one offset of Bt
+  const int nrc = Rp / kChunk;                             // chunks per offset
+
+  // ---- prologue: every load below is independent of the others, so they
+  // share one memory round trip (the row list is padded with -1, so its loads
+  // need not wait for the count)
+  const int p = tid & 3, ub = tid >> 2;  // this thread copies piece p of rows ub + 64 j
+  const int U = plan.count[tile];
+  int32_t rrow[kRowsPerLane];
+  {
+    const int32_t* rows = plan.rows + tile * kLdsRows;
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
-    const int col = n0 + nt * 16 + l16;
-    const float bv = (bias && col < N) ? bias[col] : 0.f;
+    for (int j = 0; j < kRowsPerLane; ++j) rrow[j] = rows[ub + 64 * j];
+  }
+  const int nact = plan.nact[tile];
+  const int32_t ko = tid < E ? plan.koff[tile * E + tid] : -1;
+  if (U >= kLdsRows) return;  // whole workgroup: an overflow tile
+  // byte offsets of the rows in A, kept in LDS (not registers) while the
+  // K-loop runs; the four threads of a row write the same value
+  uint32_t* s_rowoff = reinterpret_cast<uint32_t*>(smem + L.rowoff_off);
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
+  for (int j = 0; j < kRowsPerLane; ++j)
+    s_rowoff[ub + 64 * j] = rrow[j] >= 0 ? uint32_t(rrow[j]) * row_bytes : kOob;
+
+  // Staging of a chunk: issue_stage(rc) loads chunk rc of this thread's rows
+  // into registers, always all kRowsPerLane loads (out-of-range ones read
+  // zeros) so that the compiler's load counts do not depend on U; put_stage()
+  // writes them to LDS.  Chunk 0 is loaded now, chunk rc + 1 while chunk rc is
+  // multiplied.
+  frag st[kRowsPerLane];
+  auto issue_stage = [&](int rc) {
+    const int e0 = rc * kChunk + p * V;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t row = slot0 + mt * 16 + g * 4 + i;
-        const uint32_t off = (row < M && col < N)
-                                 ? uint32_t((row * N + col) * int64_t(sizeof(OutT)))
-                                 : kOob;
-        buf_store<OutT>(from_f32<OutT>(acc[mt][nt][i] + bv), ro, off);
-      }
+    for (int j = 0; j < kRowsPerLane; ++j) {
+      const uint32_t ro = s_rowoff[ub + 64 * j];
+      if (VEC)
+        st[j] = buf_frag<T>(ra, (ro != kOob && e0 < R) ? ro + uint32_t(e0) * ES : kOob);
+      else
+        st[j] = buf_frag_elems<T>(ra, ro, e0, R);
+    }
+  };
+  auto put_stage = [&]() {
+    const uint32_t wbase = L.rows_off + (chunk_base(uint32_t(ub)) ^ uint32_t(p << 4));
+#pragma unroll
+    for (int j = 0; j < kRowsPerLane; ++j)
+      if (ub + 64 * j <= U)  // rows past the zero row are not stored
+        *reinterpret_cast<frag*>(smem + wbase + 4096u * uint32_t(j)) = st[j];
+  };
+  issue_stage(0);
+  if (tid < E) s_kb[tid] = ko >= 0 ? uint32_t(ko) * k_bytes : kBOob;
+  floatx16 acc[2][2];
+  zero_acc(acc);
+  put_stage();
+  __syncthreads();
+
+  // this thread's 16-byte piece of every B slab: piece gp, column cp
+  const int gp = tid >> 6, cp = n0 + (tid & 63);
+  const uint32_t bpiece = cp < N ? uint32_t(cp) * V * ES : kColOob;
+  // this lane's 4-byte record of A addresses (rows l32 and 32 + l32 of its wave)
+  const uint32_t* arec = reinterpret_cast<const uint32_t*>(plan.addr + tile * E * kTileRows) +
+                         wave * 32 + l32;  // + item * 128 records
+
+  for (int rc = 0; rc < nrc; ++rc) {
+    const uint32_t bofs = uint32_t(rc * 4 + gp) * slab_bytes + bpiece;
+    auto gload = [&](uint32_t kb) -> uint4 {  // this thread's piece of an item's B slab
+      return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rb, kb + bofs, 0, 0));
+    };
+    auto ring_put = [&](int slot, const uint4& v) {
+      *reinterpret_cast<uint4*>(ring + uint32_t(slot) * kSlabBytes + uint32_t(tid) * 16u) = v;
+    };
+    auto read_b = [&](int slot, frag (&b)[2][2]) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          b[ks][nt] = *reinterpret_cast<const frag*>(ring + uint32_t(slot) * kSlabBytes +
+                                                     uint32_t(ks * 2 + h) * 1024u +
+                                                     uint32_t(nt * 32 + l32) * 16u);
+    };
+    auto read_a = [&](uint32_t e, frag (&a)[2][2]) {
+      const uint32_t t2[2] = {e & 0xffffu, e >> 16};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+          a[ks][mt] = *reinterpret_cast<const frag*>(rows_lds +
+                                                     (t2[mt] ^ (uint32_t(ks * 2 + h) << 4)));
+    };
+
+    // ---- pipeline.  Item i's B slab is loaded from global memory in step
+    // i-4, written to ring slot i % 3 in step i-2, read into registers in
+    // step i-1; its A addresses are loaded in step i-3 and its A fragments
+    // read in step i-1; its MFMAs run in step i.  Step `it`:
+    //   1. ring write of item it+2 (the slot was last read two steps ago),
+    //      LDS reads of the A and B fragments of item it+1, B offset of it+4,
+    //   2. the 8 MFMAs of item it (they cover the latency of the LDS work),
+    //   3. global loads of item it+4's B piece and item it+3's A addresses,
+    //   4. barrier (the ring slot written in 1 is read in the next step).
+    // Register rings of 3 (static indices, loop unrolled 3 times).
+    frag b0[2][2], b1[2][2], b2[2][2], a0[2][2], a1[2][2], a2[2][2];
+    uint4 q0, q1, q2;     // B pieces loaded, not yet in the ring
+    uint32_t r0, r1, r2;  // A address records
+    {
+      const uint32_t k0 = s_kb[0], k1 = s_kb[1], k2 = s_kb[2], k3 = s_kb[3];
+      const uint4 p0 = gload(k0), p1 = gload(k1);
+      r0 = arec[0];
+      r1 = arec[128];
+      r2 = arec[256];
+      q2 = gload(k2);
+      q0 = gload(k3);  // item 3 lives in register slot 3 % 3 = 0
+      // next chunk's rows: behind the B and A loads above, so the first items
+      // do not wait for them (past the last chunk the loads read zeros and are
+      // dropped)
+      issue_stage(rc + 1);
+      ring_put(0, p0);
+      ring_put(1, p1);
+      lds_barrier();
+      read_b(0, b0);
+      read_a(r0, a0);
+    }
+    int kb_next = 0;
+    auto step = [&](int it, frag (&bc)[2][2], frag (&bn)[2][2], frag (&ac)[2][2],
+                    frag (&an)[2][2], uint32_t rn, uint32_t& r3, const uint4& q2s, uint4& q4) {
+      ring_put((it + 2) % 3, q2s);
+      read_b((it + 1) % 3, bn);
+      read_a(rn, an);
+      kb_next = s_kb[it + 4];
+      __builtin_amdgcn_sched_barrier(0);
+      mma_item<T>(ac, bc, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      q4 = gload(uint32_t(kb_next));
+      r3 = arec[(it + 3) * 128];
+      __builtin_amdgcn_sched_barrier(0);
+      lds_barrier();
+    };
+    // register slots: A records of item i in r[i % 3], B pieces of item i in
+    // q[i % 3]; item it+4 reuses the slot of item it+1 (already in the ring)
+    step(0, b0, b1, a0, a1, r1, r0, q2, q1);
+    step(1, b1, b2, a1, a2, r2, r1, q0, q2);
+    step(2, b2, b0, a2, a0, r0, r2, q1, q0);
+    for (int it = 3; it < nact; it += 3) {  // reads items up to max(nact + 5, 6) < nact + kPad
+      step(it, b0, b1, a0, a1, r1, r0, q2, q1);
+      step(it + 1, b1, b2, a1, a2, r2, r1, q0, q2);
+      step(it + 2, b2, b0, a2, a0, r0, r2, q1, q0);
+    }
+    if (rc + 1 < nrc) {
+      put_stage();  // every wave is past the last barrier of chunk rc
+      __syncthreads();
     }
   }
+  __syncthreads();  // staged rows and ring are free for the epilogue
+  store_tile<OutT>(acc, bias, ro, rows_lds + uint32_t(wave) * 64u * epi_pitch(sizeof(OutT)), slot0,
+                   n0, M, N, lane);
 }

@@ -5,20 +5,20 @@
 //
 //   out[m, n] = bias[n] + sum_k sum_r A[pairs[k, m], r] * B[k][n][r]
 //
-// Work split: a workgroup is 4 waves; each wave owns 64 output rows x 64
-// output columns = 2 x 2 tiles of v_mfma_f32_32x32x16_{f16,bf16} (or
-// v_mfma_f32_32x32x2f32 for fp32).  A rows are gathered straight from global
-// memory into the MFMA A operand: lane l holds row (l % 32) and 16 contiguous
-// bytes of the reduction dimension, so a gather is one 16-byte load per lane.
-// B (the weights) is relaid once per call into [k][r / V][n][V] (V elements
-// = 16 bytes), which makes every B operand load a fully coalesced 1 KiB read.
-// Any assignment of reduction indices to (MFMA step, lane half, element) is
-// valid as long as A and B use the same one; both use r = r0 + half*V + e.
+// The kernel itself (sp_gather_gemm.h): a workgroup owns 256 output rows x 64
+// output columns, a wave 64 x 64 as 4 x 4 tiles of 16x16 MFMAs.  Gathered A
+// rows come from LDS, where the tile's distinct source rows are staged once
+// per K-step using a gather plan (sp_plan.h), or straight from global memory
+// when there is no plan.  B (the weights) is relaid once into [k][r / V][n][V]
+// (V elements = 16 bytes), which makes every B operand load a coalesced 1 KiB
+// read.  Any assignment of reduction indices to (MFMA step, lane group,
+// element) is valid as long as A and B use the same one.
 //
-// Masked mode (MaskImplicitGemm, gemm.py:282-296): rows are visited in
-// mask_argsort order; the OR of the 64 rows' offset bitmasks is taken with
-// a wave reduction and offsets empty for the whole wave tile are skipped.
-// Skipped terms are exactly zero, so the result equals the dense one.
+// Masked mode (MaskImplicitGemm, gemm.py:282-296): the reference visits rows in
+// mask_argsort order to skip offsets that are empty for a whole tile.  Here the
+// kernel skips such offsets per 64-row wave tile by itself (a ballot over the
+// rows' pairs) and keeps the rows' natural order; skipped terms are exactly
+// zero, so the result equals the dense one.
 //
 // Weight gradient (gemm.py:324-426): per offset k, dW[k] = X_k^T G_k over the
 // compacted pairs of that offset.  The pair dimension is the MFMA reduction
@@ -27,6 +27,7 @@
 // into `splits` contiguous ranges whose fp32 partials are summed in a fixed
 // order by a second kernel (deterministic, no atomics).
 #include "sp_common.h"
+#include "sp_plan.h"
 
 namespace sp {
 
@@ -286,75 +287,121 @@ static int pack_weight(const void* w, int w_dtype, const void* bias, int64_t K, 
   return SP_OK;
 }
 
-template <typename T, typename OutT, bool VEC, int RS>
-static void launch_one(dim3 grid, hipStream_t s, const T* A, const T* bt, const int32_t* pairs,
-                       const float* bias, OutT* o, GemmBufs nb, int64_t n_src, int64_t M, int N,
-                       int R, int Rp, int kv) {
-  gather_gemm<T, OutT, VEC, RS><<<grid, 256, 0, s>>>(A, bt, pairs, bias, o, nb, n_src, M, N, R,
-                                                    Rp, kv);
+// Launch description shared by the typed launchers.
+struct GemmCall {
+  int64_t n_src, M;
+  int N, R, Rp, kv;
+  bool planned;
+  PlanDev plan;
+  int64_t n_overflow;  // overflow tiles of the plan (run by the direct kernel)
+  const float* bias;
+  bool vec;
+};
+
+// Raises a kernel's dynamic LDS limit to `bytes` (once per kernel and process).
+static int allow_lds(const void* kern, uint32_t bytes, bool& done) {
+  if (!done) {
+    SP_HIP(hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)));
+    done = true;
+  }
+  return SP_OK;
 }
 
-// The mask tables (pair_mask / mask_argsort) of the reference's masked path
-// are accepted but not needed: the kernel skips offsets that are empty for a
-// whole tile by itself and keeps rows in their natural order (better locality
-// for the gathers, the pair-table reads and the output writes).
-template <typename T, typename OutT>
-static int launch_gemm_typed(const T* A, int64_t n_src, const T* bt, const int32_t* pairs,
-                             const int32_t* pm, const int32_t* ar, const float* bias, void* out,
-                             int64_t M, int N, int R, int Rp, int kv, bool vec, hipStream_t s) {
-  (void)pm;
-  (void)ar;
-  const int64_t gx = cdiv(M, 256);
-  SP_CHECK_ARG(gx <= kMaxGridX, "gemm: too many rows");
-  // buffer instructions take 32-bit byte offsets
-  const int64_t lim = int64_t(kOob);
-  const int64_t a_bytes = n_src * R * int64_t(sizeof(T));
-  const int64_t bt_bytes = int64_t(kv) * Rp * N * int64_t(sizeof(T));
-  const int64_t p_bytes = int64_t(kv) * M * 4;
-  const int64_t o_bytes = M * N * int64_t(sizeof(OutT));
-  if (a_bytes >= lim || bt_bytes >= lim || p_bytes >= lim || o_bytes >= lim)
-    return set_error(SP_ERR_UNSUPPORTED,
-                     "gemm: a tensor exceeds 4 GiB (features %lld B, pairs %lld B, out %lld B)",
-                     (long long)a_bytes, (long long)p_bytes, (long long)o_bytes);
-  GemmBufs nb{uint32_t(a_bytes), uint32_t(bt_bytes), uint32_t(p_bytes), uint32_t(o_bytes)};
-  const dim3 grid{unsigned(gx), unsigned(cdiv(N, 64)), 1u};
-  OutT* o = static_cast<OutT*>(out);
-  const int steps = Rp / M16<T>::KSTEP;
-  if (!vec)
-    launch_one<T, OutT, false, 1>(grid, s, A, bt, pairs, bias, o, nb, n_src, M, N, R, Rp, kv);
-  else if (steps % 4 == 0)
-    launch_one<T, OutT, true, 4>(grid, s, A, bt, pairs, bias, o, nb, n_src, M, N, R, Rp, kv);
-  else if (steps % 2 == 0)
-    launch_one<T, OutT, true, 2>(grid, s, A, bt, pairs, bias, o, nb, n_src, M, N, R, Rp, kv);
-  else
-    launch_one<T, OutT, true, 1>(grid, s, A, bt, pairs, bias, o, nb, n_src, M, N, R, Rp, kv);
+template <typename T, typename OutT, bool VEC>
+static int launch_direct(dim3 grid, hipStream_t s, const T* A, const T* bt, const int32_t* pairs,
+                         OutT* o, GemmBufs nb, const GemmCall& c, PlanDev plan) {
+  const int G = c.kv < kGroupOffsets ? c.kv : kGroupOffsets;
+  const uint32_t lds = direct_lds(G + kPad, uint32_t(sizeof(OutT))).total;
+  auto kern = gather_gemm_direct<T, OutT, VEC>;
+  static bool attr_set = false;
+  int rc = allow_lds(reinterpret_cast<const void*>(kern),
+                     direct_lds(kGroupOffsets + kPad, uint32_t(sizeof(OutT))).total, attr_set);
+  if (rc) return rc;
+  kern<<<grid, 256, lds, s>>>(A, bt, pairs, plan, c.bias, o, nb, c.n_src, c.M, c.N, c.R, c.Rp,
+                              c.kv);
   SP_LAUNCHED();
   return SP_OK;
 }
 
+template <typename T, typename OutT, bool VEC>
+static int launch_staged(dim3 grid, hipStream_t s, const T* A, const T* bt, OutT* o, GemmBufs nb,
+                         const GemmCall& c) {
+  const uint32_t lds = staged_lds(c.kv + kPad, uint32_t(sizeof(OutT))).total;
+  auto kern = gather_gemm_staged<T, OutT, VEC>;
+  static bool attr_set = false;
+  int rc = allow_lds(reinterpret_cast<const void*>(kern),
+                     staged_lds(kPlanMaxKv + kPad, uint32_t(sizeof(OutT))).total, attr_set);
+  if (rc) return rc;
+  kern<<<grid, 256, lds, s>>>(A, bt, c.plan, c.bias, o, nb, c.M, c.N, c.R, c.Rp, c.kv);
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+// Planned call: the staged kernel over all tiles (it skips overflow tiles),
+// then the direct kernel over the overflow list when there is one.
+// Unplanned call: the direct kernel over all tiles.
+template <typename T, typename OutT, bool VEC>
+static int launch_modes(unsigned gx, unsigned gy, hipStream_t s, const T* A, const T* bt,
+                        const int32_t* pairs, OutT* o, GemmBufs nb, const GemmCall& c) {
+  const PlanDev none{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0};
+  if (!c.planned)
+    return launch_direct<T, OutT, VEC>(dim3{gx, gy, 1u}, s, A, bt, pairs, o, nb, c, none);
+  int rc = launch_staged<T, OutT, VEC>(dim3{gx, gy, 1u}, s, A, bt, o, nb, c);
+  if (rc || c.n_overflow == 0) return rc;
+  return launch_direct<T, OutT, VEC>(dim3{unsigned(c.n_overflow), gy, 1u}, s, A, bt, pairs, o, nb,
+                                     c, c.plan);
+}
+
+// The mask tables (pair_mask / mask_argsort) of the reference's masked path
+// are accepted but not needed: the kernel skips offsets that are empty for a
+// whole wave tile by itself and keeps rows in their natural order (better
+// locality for the gathers, the table reads and the output writes).
+template <typename T, typename OutT>
+static int launch_gemm_typed(const T* A, const T* bt, const int32_t* pairs, void* out,
+                             const GemmCall& c, hipStream_t s) {
+  const int64_t gx = cdiv(c.M, kTileRows);
+  SP_CHECK_ARG(gx <= kMaxGridX, "gemm: too many rows");
+  // buffer instructions take 32-bit byte offsets
+  const int64_t lim = int64_t(kOob);
+  const int64_t a_bytes = c.n_src * c.R * int64_t(sizeof(T));
+  const int64_t bt_bytes = int64_t(c.kv) * c.Rp * c.N * int64_t(sizeof(T));
+  const int64_t p_bytes = int64_t(c.kv) * c.M * 4;
+  const int64_t o_bytes = c.M * c.N * int64_t(sizeof(OutT));
+  if (a_bytes >= lim || bt_bytes >= lim || p_bytes >= lim || o_bytes >= lim)
+    return set_error(SP_ERR_UNSUPPORTED,
+                     "gemm: a tensor exceeds 4 GiB (features %lld B, pairs %lld B, out %lld B)",
+                     (long long)a_bytes, (long long)p_bytes, (long long)o_bytes);
+  if (bt_bytes >= int64_t(kMaxBtBytes))
+    return set_error(SP_ERR_UNSUPPORTED, "gemm: packed weights of %lld B exceed 1 GiB",
+                     (long long)bt_bytes);
+  GemmBufs nb{uint32_t(a_bytes), uint32_t(bt_bytes), uint32_t(p_bytes), uint32_t(o_bytes)};
+  const unsigned gy = unsigned(cdiv(c.N, 64));
+  OutT* o = static_cast<OutT*>(out);
+  if (c.vec) return launch_modes<T, OutT, true>(unsigned(gx), gy, s, A, bt, pairs, o, nb, c);
+  return launch_modes<T, OutT, false>(unsigned(gx), gy, s, A, bt, pairs, o, nb, c);
+}
+
 template <typename T>
-static int launch_gemm_out(int out_dtype, const T* A, int64_t n_src, const T* bt,
-                           const int32_t* pairs, const int32_t* pm, const int32_t* ar,
-                           const float* bias, void* out, int64_t M, int N, int R, int Rp, int kv,
-                           bool vec, hipStream_t s) {
+static int launch_gemm_out(int out_dtype, const T* A, const T* bt, const int32_t* pairs,
+                           void* out, const GemmCall& c, hipStream_t s) {
   switch (out_dtype) {
     case SP_F16:
-      return launch_gemm_typed<T, _Float16>(A, n_src, bt, pairs, pm, ar, bias, out, M, N, R, Rp,
-                                            kv, vec, s);
+      return launch_gemm_typed<T, _Float16>(A, bt, pairs, out, c, s);
     case SP_BF16:
-      return launch_gemm_typed<T, __bf16>(A, n_src, bt, pairs, pm, ar, bias, out, M, N, R, Rp, kv,
-                                          vec, s);
+      return launch_gemm_typed<T, __bf16>(A, bt, pairs, out, c, s);
     case SP_F32:
-      return launch_gemm_typed<T, float>(A, n_src, bt, pairs, pm, ar, bias, out, M, N, R, Rp, kv,
-                                         vec, s);
+      return launch_gemm_typed<T, float>(A, bt, pairs, out, c, s);
     default:
       return set_error(SP_ERR_UNSUPPORTED, "gemm: output dtype %d not supported", out_dtype);
   }
 }
 
+// plan (nullable) is a gather plan of `pairs` built by sp_gather_plan_build,
+// which reported n_overflow.
 static int gemm_packed(const void* A, int dtype, int64_t n_src, const void* packed, int64_t K,
                        int64_t kv, int64_t C, int transpose, int has_bias, const int32_t* pairs,
-                       int64_t M, const int32_t* pm, const int32_t* ar, void* out, int out_dtype,
+                       int64_t M, const int32_t* pm, const int32_t* ar, const void* plan,
+                       size_t plan_bytes, int64_t n_overflow, void* out, int out_dtype,
                        hipStream_t s) {
   SP_CHECK_ARG(gemm_dtype_ok(dtype), "gemm: feature dtype %d not supported (f16/bf16/f32)", dtype);
   SP_CHECK_ARG(K >= 1 && C >= 1 && kv >= 1 && M >= 0 && n_src >= 0, "gemm: bad sizes");
@@ -365,22 +412,39 @@ static int gemm_packed(const void* A, int dtype, int64_t n_src, const void* pack
   SP_CHECK_ARG(A && packed && pairs && out, "gemm: null pointer");
   const Packed p = packed_layout(K, kv, C, dtype, transpose);
   const char* base = static_cast<const char*>(packed);
-  const float* bias = has_bias ? reinterpret_cast<const float*>(base + p.bias_off) : nullptr;
-  const int V = vec_of(dtype);
-  const bool vec = (p.R % V == 0) && (reinterpret_cast<uintptr_t>(A) % 16 == 0);
+  GemmCall c;
+  c.n_src = n_src;
+  c.M = M;
+  c.N = p.N;
+  c.R = p.R;
+  c.Rp = p.Rp;
+  c.kv = int(kv);
+  c.bias = has_bias ? reinterpret_cast<const float*>(base + p.bias_off) : nullptr;
+  c.vec = (p.R % vec_of(dtype) == 0) && (reinterpret_cast<uintptr_t>(A) % 16 == 0);
+  c.planned = plan != nullptr;
+  c.plan = PlanDev{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0};
+  c.n_overflow = 0;
+  if (plan) {
+    SP_CHECK_ARG(kv <= kPlanMaxKv, "gemm: gather plans need kv <= %d", kPlanMaxKv);
+    const PlanLayout pl = plan_layout(M, kv);
+    SP_CHECK_ARG(plan_bytes >= pl.total, "gemm: plan buffer %zu < %zu bytes", plan_bytes,
+                 pl.total);
+    SP_CHECK_ARG(n_overflow >= 0 && n_overflow <= pl.ntiles,
+                 "gemm: n_overflow %lld outside 0..%lld", (long long)n_overflow,
+                 (long long)pl.ntiles);
+    c.plan = plan_view(plan, M, kv);
+    c.n_overflow = n_overflow;
+  }
   switch (dtype) {
     case SP_F16:
-      return launch_gemm_out<_Float16>(out_dtype, static_cast<const _Float16*>(A), n_src,
-                                       reinterpret_cast<const _Float16*>(base), pairs, pm, ar,
-                                       bias, out, M, p.N, p.R, p.Rp, int(kv), vec, s);
+      return launch_gemm_out<_Float16>(out_dtype, static_cast<const _Float16*>(A),
+                                       reinterpret_cast<const _Float16*>(base), pairs, out, c, s);
     case SP_BF16:
-      return launch_gemm_out<__bf16>(out_dtype, static_cast<const __bf16*>(A), n_src,
-                                     reinterpret_cast<const __bf16*>(base), pairs, pm, ar, bias,
-                                     out, M, p.N, p.R, p.Rp, int(kv), vec, s);
+      return launch_gemm_out<__bf16>(out_dtype, static_cast<const __bf16*>(A),
+                                     reinterpret_cast<const __bf16*>(base), pairs, out, c, s);
     default:
-      return launch_gemm_out<float>(out_dtype, static_cast<const float*>(A), n_src,
-                                    reinterpret_cast<const float*>(base), pairs, pm, ar, bias, out,
-                                    M, p.N, p.R, p.Rp, int(kv), vec, s);
+      return launch_gemm_out<float>(out_dtype, static_cast<const float*>(A),
+                                    reinterpret_cast<const float*>(base), pairs, out, c, s);
   }
 }
 
@@ -398,7 +462,7 @@ static int gemm_common(const void* A, int dtype, int64_t n_src, const void* w, i
   int rc = pack_weight(w, w_dtype, bias, K, kv, C, dtype, transpose, ws, s);
   if (rc) return rc;
   return gemm_packed(A, dtype, n_src, ws, K, kv, C, transpose, bias != nullptr, pairs, M, pm, ar,
-                     out, out_dtype, s);
+                     nullptr, 0, 0, out, out_dtype, s);
 }
 
 static int wgrad_splits(int64_t kv, int64_t C, int64_t K, int64_t n_rows) {
@@ -438,7 +502,16 @@ int sp_conv_gemm_packed(const void* a, int32_t dtype, int64_t n_src, const void*
                         const int32_t* pairs, int64_t M, const int32_t* pair_mask,
                         const int32_t* mask_argsort, void* out, int32_t out_dtype, void* stream) {
   return gemm_packed(a, dtype, n_src, packed, K, kv, C, transpose, has_bias, pairs, M, pair_mask,
-                     mask_argsort, out, out_dtype, as_stream(stream));
+                     mask_argsort, nullptr, 0, 0, out, out_dtype, as_stream(stream));
+}
+
+int sp_conv_gemm_planned(const void* a, int32_t dtype, int64_t n_src, const void* packed,
+                         int64_t K, int64_t kv, int64_t C, int32_t transpose, int32_t has_bias,
+                         const int32_t* pairs, int64_t M, const void* plan, size_t plan_bytes,
+                         int64_t n_overflow, void* out, int32_t out_dtype, void* stream) {
+  SP_CHECK_ARG(plan != nullptr, "gemm: null gather plan");
+  return gemm_packed(a, dtype, n_src, packed, K, kv, C, transpose, has_bias, pairs, M, nullptr,
+                     nullptr, plan, plan_bytes, n_overflow, out, out_dtype, as_stream(stream));
 }
 
 int sp_conv_fwd(const void* x, int32_t dtype, int64_t n_in, int64_t C, const void* w,

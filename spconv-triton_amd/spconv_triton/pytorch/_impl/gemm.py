@@ -15,6 +15,7 @@ least as accurate.  The flags are still accepted.
 
 from __future__ import annotations
 
+import ctypes
 import weakref
 
 import torch
@@ -88,12 +89,54 @@ def packed_weight(filters: torch.Tensor, bias: torch.Tensor | None, dtype: torch
     return packed
 
 
+#: Use gather plans (per-tile distinct source rows staged in LDS) for the
+#: forward and input-gradient GEMMs.  Results are bit-identical either way;
+#: tests switch this off to compare the two kernels' modes.
+USE_GATHER_PLAN = True
+
+
+def gather_plan(pairs: torch.Tensor, n_src: int):
+    """Gather plan of a [kv, M] pair table (``sp_gather_plan_build``) as
+    (plan buffer, number of overflow tiles), or None when kv is outside the
+    planned kernel's range.  Memoised on the table tensor, like the reference
+    memoises its tables on the indice data (pairs.py:429-469); rebuilt if the
+    table is modified in place.  Building synchronizes the stream once."""
+    kv, M = pairs.shape
+    cached = getattr(pairs, "_spconv_triton_plan", None)
+    stamp = (int(n_src), pairs._version, pairs.data_ptr())
+    if cached is not None and cached[0] == stamp:
+        return cached[1]
+    L = _lib.lib()
+    nbytes = L.sp_gather_plan_bytes(M, kv)
+    if nbytes == 0:
+        return None
+    plan = torch.empty(nbytes, dtype=torch.uint8, device=pairs.device)
+    n_over = ctypes.c_int64(0)
+    _lib.check(L.sp_gather_plan_build(_lib.ptr(pairs), kv, M, int(n_src), _lib.ptr(plan), nbytes,
+                                      ctypes.byref(n_over), _lib.stream_of(pairs.device)),
+               "sp_gather_plan_build")
+    res = (plan, int(n_over.value))
+    pairs._spconv_triton_plan = (stamp, res)
+    return res
+
+
 def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: torch.Tensor,
           M: int, pm, ar, out: torch.Tensor):
     K, C = filters.shape[0], filters.shape[-1]
     kv = pairs.shape[0]
     packed = packed_weight(filters, bias, a.dtype, transpose)
-    _lib.check(_lib.lib().sp_conv_gemm_packed(
+    L = _lib.lib()
+    planned = gather_plan(pairs, a.shape[0]) if USE_GATHER_PLAN else None
+    if planned is not None:
+        # the planned kernel skips empty offsets itself: mask tables are not needed
+        plan, n_over = planned
+        _lib.check(L.sp_conv_gemm_planned(
+            _lib.ptr(a), _lib.dtype_code(a.dtype), a.shape[0], _lib.ptr(packed), K, kv, C,
+            int(transpose), int(bias is not None), _lib.ptr(pairs), M, _lib.ptr(plan),
+            plan.numel(), n_over, _lib.ptr(out), _lib.dtype_code(out.dtype),
+            _lib.stream_of(a.device)), "sp_conv_gemm_planned")
+        return
+    _lib.check(L.sp_conv_gemm_packed(
         _lib.ptr(a), _lib.dtype_code(a.dtype), a.shape[0], _lib.ptr(packed), K, kv, C,
         int(transpose), int(bias is not None), _lib.ptr(pairs), M, _lib.ptr(pm), _lib.ptr(ar),
         _lib.ptr(out), _lib.dtype_code(out.dtype), _lib.stream_of(a.device)),

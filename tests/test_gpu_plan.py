@@ -1,0 +1,215 @@
+"""Gather plans and the planned gather-GEMM.
+
+A gather plan lists, per tile of 256 consecutive rows of a [kv, M] pair table,
+the ascending distinct source rows, and per 64-row wave tile the offsets with
+a pair and the staged LDS address of every (offset, row) (csrc/sp_plan.h).
+The plan is checked entry by entry against numpy (``np.unique`` /
+``np.searchsorted`` per tile).  The planned GEMM stages those
+rows in LDS; it must be bit-identical to the unplanned GEMM (same summation
+order by construction) on every dtype, on rows whose length is not a multiple
+of the vector width, on several column blocks, on the input gradient, and on
+tiles with too many distinct rows for LDS (which the kernel gathers directly).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_gemm import CASES, _q, _tables, rand_indices
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+TILE = 256
+LDS_ROWS = 960  # kLdsRows of csrc/sp_plan.h
+PAD = 7  # kPad of csrc/sp_plan.h
+
+
+def _align(v, a=256):
+    return (v + a - 1) // a * a
+
+
+def _chunk_base(slot):
+    """LDS address of a staged row (slot * 64, 16-byte pieces xor-swizzled by slot bits 2-3)."""
+    slot = np.asarray(slot, dtype=np.int64)
+    return slot * 64 + (((slot >> 2) & 3) << 4)
+
+
+def _parse(plan, kv, M):
+    """Split a plan buffer into its parts (layout of csrc/sp_plan.h)."""
+    nt = (max(M, 1) + TILE - 1) // TILE
+    E = kv + PAD
+    buf = plan.cpu().numpy()
+    count_off = 256
+    ovf_off = _align(count_off + nt * 4)
+    rows_off = _align(ovf_off + nt * 4)
+    nact_off = _align(rows_off + nt * LDS_ROWS * 4)
+    koff_off = _align(nact_off + nt * 4)
+    addr_off = _align(koff_off + nt * E * 4)
+    n_ovf = int(buf[:4].view(np.int32)[0])
+    return {
+        "n_ovf": n_ovf,
+        "count": buf[count_off:count_off + nt * 4].view(np.int32),
+        "ovf": buf[ovf_off:ovf_off + nt * 4].view(np.int32)[:n_ovf],
+        "rows": buf[rows_off:rows_off + nt * LDS_ROWS * 4].view(np.int32).reshape(nt, LDS_ROWS),
+        "nact": buf[nact_off:nact_off + nt * 4].view(np.int32),
+        "koff": buf[koff_off:koff_off + nt * E * 4].view(np.int32).reshape(nt, E),
+        # [tile][item][wave][l32][mt] -> [tile][item][row of the tile]
+        "addr": buf[addr_off:addr_off + nt * E * TILE * 2].view(np.uint16)
+                .reshape(nt, E, 4, 32, 2).transpose(0, 1, 2, 4, 3).reshape(nt, E, TILE),
+    }
+
+
+def _check_plan(pf, n_src):
+    """Every part of the plan against numpy: per tile np.unique of the valid
+    sources, the offsets with a pair (ascending) then padding, and per (item,
+    row) the staged address of the row's rank in the unique list
+    (np.searchsorted), or of the zero row U."""
+    from spconv_triton.pytorch._impl import gemm
+
+    kv, M = pf.shape
+    res = gemm.gather_plan(pf, n_src)
+    assert res is not None
+    plan, n_over_host = res
+    P = _parse(plan, kv, M)
+    p = pf.cpu().numpy()
+    overflow = []
+    for t in range((M + TILE - 1) // TILE):
+        blk = p[:, t * TILE:(t + 1) * TILE]
+        valid = (blk >= 0) & (blk < n_src)
+        uniq = np.unique(blk[valid])
+        U = uniq.size
+        assert P["count"][t] == U, f"tile {t}: count {P['count'][t]} != {U}"
+        if U >= LDS_ROWS:
+            overflow.append(t)
+            continue
+        np.testing.assert_array_equal(P["rows"][t, :U], uniq)
+        assert (P["rows"][t, U:] == -1).all()
+        addr = np.where(valid, _chunk_base(np.searchsorted(uniq, np.where(valid, blk, 0))),
+                        _chunk_base(U))
+        live = np.nonzero(valid.any(axis=1))[0]
+        n = live.size
+        assert P["nact"][t] == n, f"tile {t}: {P['nact'][t]} items != {n}"
+        np.testing.assert_array_equal(P["koff"][t, :n], live)
+        assert (P["koff"][t, n:n + PAD] == -1).all()
+        exp = np.full((n + PAD, TILE), _chunk_base(U), dtype=np.int64)
+        a = addr[live]
+        exp[:n, :a.shape[1]] = a  # rows past M (last tile) keep the zero row
+        np.testing.assert_array_equal(P["addr"][t, :n + PAD].astype(np.int64), exp)
+    assert n_over_host == P["n_ovf"] == len(overflow)
+    np.testing.assert_array_equal(P["ovf"], np.asarray(overflow, dtype=np.int32))
+    return len(overflow)
+
+
+def _random_table(rng, kv, M, n_src, p_valid):
+    t = rng.integers(0, n_src, size=(kv, M)).astype(np.int32)
+    t[rng.random((kv, M)) > p_valid] = -1
+    return torch.from_numpy(t).to(DEV)
+
+
+def test_plan_layout_limits():
+    from spconv_triton.pytorch._impl import _lib
+
+    L = _lib.lib()
+    assert L.sp_gather_plan_bytes(1000, 64) > 0
+    assert L.sp_gather_plan_bytes(1000, 65) == 0  # kv above the planned kernel's range
+    assert L.sp_gather_plan_bytes(1000, 0) == 0
+
+
+@pytest.mark.parametrize("case", ["subm", "strided_fwd", "strided_bwd", "tiny", "exact_tiles",
+                                  "overflow", "kv64"])
+def test_plan_matches_numpy(case):
+    rng = np.random.default_rng(7)
+    if case in ("subm", "strided_fwd", "strided_bwd"):
+        idx = rand_indices(rng, 2, [28] * 3, 6000)
+        subm = case == "subm"
+        res = _tables(idx, 2, [28] * 3, [3] * 3, [1 if subm else 2] * 3, [1] * 3, subm)
+        if case == "strided_bwd":
+            pf, n_src = res[3], res[2].shape[1]
+        else:
+            pf, n_src = res[2], idx.shape[0]
+    elif case == "tiny":
+        idx = rand_indices(rng, 1, [8] * 3, 100)
+        pf, n_src = _tables(idx, 1, [8] * 3, [3] * 3, [1] * 3, [1] * 3, True)[2], 100
+    elif case == "exact_tiles":
+        pf, n_src = _random_table(rng, 27, 512, 800, 0.3), 800
+    elif case == "overflow":
+        pf, n_src = _random_table(rng, 27, 700, 100_000, 0.7), 100_000
+    else:
+        pf, n_src = _random_table(rng, 64, 600, 900, 0.2), 900
+    n_over = _check_plan(pf.contiguous(), n_src)
+    if case == "overflow":
+        assert n_over == 3
+    if case == "tiny":
+        assert n_over == 0
+
+
+def _both(a, w, bias, transpose, pairs, M, out_dtype=None):
+    from spconv_triton.pytorch._impl import gemm
+
+    out_dtype = out_dtype or a.dtype
+    N = w.shape[-1] if transpose else w.shape[0]
+    res = []
+    for use in (True, False):
+        gemm.USE_GATHER_PLAN = use
+        try:
+            out = torch.empty((M, N), dtype=out_dtype, device=DEV)
+            gemm._gemm(a, w, bias, transpose, pairs, M, None, None, out)
+            res.append(out)
+        finally:
+            gemm.USE_GATHER_PLAN = True
+    return res
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("ci", range(len(CASES)))
+def test_planned_equals_unplanned(ci, dtype):
+    C, K, n, subm, stride = CASES[ci]
+    rng = np.random.default_rng(90 + ci)
+    idx = rand_indices(rng, 2, [28] * 3, n)
+    res = _tables(idx, 2, [28] * 3, [3] * 3, [stride] * 3, [1] * 3, subm)
+    pf, pb = res[2], res[3]
+    torch.manual_seed(ci)
+    x, _ = _q(torch.randn(idx.shape[0], C), dtype)
+    w, _ = _q(torch.randn(K, 3, 3, 3, C) / np.sqrt(27 * C), dtype)
+    b, _ = _q(torch.randn(K) * 0.1, dtype)
+    planned, direct = _both(x, w, b, False, pf, pf.shape[1])
+    assert torch.equal(planned, direct), "forward: planned != unplanned"
+    g, _ = _q(torch.randn(pf.shape[1], K), dtype)
+    planned, direct = _both(g, w, None, True, pb, idx.shape[0])
+    assert torch.equal(planned, direct), "dgrad: planned != unplanned"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_planned_overflow_tiles(dtype):
+    """Tiles with >= 1023 distinct rows take the direct gather inside the planned
+    kernel; mixed with staged tiles the result must not change."""
+    rng = np.random.default_rng(11)
+    kv, M, n_src, C, K = 27, 1500, 50_000, 32, 64
+    t = rng.integers(0, n_src, size=(kv, M)).astype(np.int32)
+    t[rng.random((kv, M)) > 0.6] = -1
+    # tiles 2..5 reference only a narrow window of rows: they fit in LDS
+    t[:, 512:] = np.where(t[:, 512:] >= 0, t[:, 512:] % 600, -1)
+    pf = torch.from_numpy(t).to(DEV)
+    assert _check_plan(pf, n_src) == 2
+    torch.manual_seed(5)
+    x, _ = _q(torch.randn(n_src, C), dtype)
+    w, _ = _q(torch.randn(K, kv, C) * 0.05, dtype)
+    planned, direct = _both(x, w, None, False, pf, M)
+    assert torch.equal(planned, direct)
+
+
+def test_planned_metric_shape():
+    """The benchmark layer's shape: 200k-voxel surface cloud, 64 -> 64, fp16."""
+    from bench_data import surface_cloud
+
+    idx = surface_cloud(200_000, 256, seed=0)
+    res = _tables(idx, 1, [256] * 3, [3] * 3, [1] * 3, [1] * 3, True)
+    pf = res[2]
+    assert _check_plan(pf, idx.shape[0]) == 0
+    torch.manual_seed(0)
+    x = torch.randn(idx.shape[0], 64, device=DEV).half()
+    w = (torch.randn(64, 3, 3, 3, 64, device=DEV) * 0.03).half()
+    b = torch.randn(64, device=DEV).half()
+    planned, direct = _both(x, w, b, False, pf, pf.shape[1])
+    assert torch.equal(planned, direct)
