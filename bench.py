@@ -8,7 +8,9 @@ cached under its indice_key (the reference times subm "with the neighborhood
 map cached & reused"); steps are replayed from a HIP graph so the GPU, not the
 Python host, is measured.  Also reported:
 
-* pairgen_ms: cold build of the subm rulebook (hash build + probe + mask sort);
+* pairgen_ms: cold build of the subm rulebook (hash build + probe + mask sort)
+  plus the gather plan the GEMM stages its rows with (both are built once per
+  rulebook and reused by every layer sharing the indice_key);
 * eager_ms: the same forward called from Python without a graph;
 * roofline: the gather-GEMM kernel's algorithmic bytes per launch over its
   average launch time (HIP events on the stream it runs on);
@@ -52,11 +54,30 @@ def build_layer(torch, spconv, dev):
     return conv.to(dev).half().eval()
 
 
-def gemm_bytes(n_in: int, n_out: int) -> int:
+def gemm_bytes(n_in: int, n_out: int, plan_bytes: int) -> int:
     """Algorithmic HBM bytes of one forward launch: features read once, output
-    written once, weights once, and the dense [kv, n_out] int32 gather table."""
+    written once, weights once, and the gather-plan entries the kernel needs
+    (see plan_read_bytes)."""
     e = 2
-    return e * (n_in * C_IN + n_out * C_OUT + KV * C_IN * C_OUT) + 4 * KV * n_out
+    return e * (n_in * C_IN + n_out * C_OUT + KV * C_IN * C_OUT) + plan_bytes
+
+
+def plan_read_bytes(plan, kv: int, n_out: int) -> int:
+    """Bytes of the gather plan the staged kernel must read: per tile its
+    distinct-row list (4 B per row) and, per item, one uint16 LDS address per
+    output row (csrc/sp_plan.h layout)."""
+    import numpy as np
+
+    tile = 256
+    nt = (n_out + tile - 1) // tile
+    buf = plan.cpu().numpy()
+    count = buf[256:256 + nt * 4].view(np.int32)
+    align = lambda v: (v + 255) // 256 * 256
+    ovf_off = align(256 + nt * 4)
+    rows_off = align(ovf_off + nt * 4)
+    nact_off = align(rows_off + nt * 960 * 4)
+    nact = buf[nact_off:nact_off + nt * 4].view(np.int32)
+    return int(count.astype(np.int64).sum() * 4 + nact.astype(np.int64).sum() * tile * 2)
 
 
 def cpu_baseline(idx, feats_np, w_np, b_np, pf_np):
@@ -121,7 +142,7 @@ def main() -> int:
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the sparse-conv hot path shards by batch sample; see DESIGN.md)",
+              "(the sparse-conv hot path would shard by batch sample)",
               file=sys.stderr)
         return 2
 
@@ -132,6 +153,7 @@ def main() -> int:
     from bench_data import surface_cloud
     from spconv_triton.core import ConvAlgo
     from spconv_triton.pytorch import ops
+    from spconv_triton.pytorch._impl import gemm as gemm_impl
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
@@ -142,7 +164,7 @@ def main() -> int:
     feats = torch.randn(N_VOXELS, C_IN, device=dev).half()
     conv = build_layer(torch, spconv, dev)
 
-    # ---- cold pair generation -------------------------------------------
+    # ---- cold pair generation (rulebook + gather plan) ---------------------
     def pairgen():
         return ops.get_indice_pairs_implicit_gemm(idx, 1, [GRID] * 3, ConvAlgo.MaskImplicitGemm,
                                                   [3] * 3, [1] * 3, [1] * 3, [1] * 3, [0] * 3,
@@ -151,16 +173,21 @@ def main() -> int:
     log("pair generation")
     for _ in range(5):
         res = pairgen()
+        gemm_impl.gather_plan(res[2], N_VOXELS)
     torch.cuda.synchronize()
-    pg = []
+    pg, pg_rules = [], []
     for _ in range(30):
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s, m, e = (torch.cuda.Event(enable_timing=True) for _ in range(3))
         s.record()
         res = pairgen()
+        m.record()
+        gemm_impl.gather_plan(res[2], N_VOXELS)  # synchronizes once (overflow count)
         e.record()
         torch.cuda.synchronize()
         pg.append(s.elapsed_time(e))
+        pg_rules.append(s.elapsed_time(m))
     pairgen_ms = statistics.median(pg)
+    rules_ms = statistics.median(pg_rules)
     pf = res[2]
     n_pairs = int((pf >= 0).sum().item())
 
@@ -223,7 +250,8 @@ def main() -> int:
     tfile = ROOT / "profiles" / "gather_gemm_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
-    nbytes = gemm_bytes(N_VOXELS, N_VOXELS)
+    plan, n_overflow = gemm_impl.gather_plan(y0.indice_dict["subm0"].pair_fwd, N_VOXELS)
+    nbytes = gemm_bytes(N_VOXELS, N_VOXELS, plan_read_bytes(plan, KV, N_VOXELS))
     flops = 2.0 * n_pairs * C_IN * C_OUT
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
     mvox = N_VOXELS / (ms_per_step * 1e-3) / 1e6
@@ -258,6 +286,9 @@ def main() -> int:
         "fwd_ms": round(ms_per_step, 5),
         "eager_ms": round(eager_ms, 5),
         "pairgen_ms": round(pairgen_ms, 4),
+        "pairgen_parts_ms": {"rulebook": round(rules_ms, 4),
+                             "gather_plan": round(pairgen_ms - rules_ms, 4)},
+        "overflow_tiles": int(n_overflow),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 1),
@@ -265,7 +296,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "kernel": "gather_gemm<f16,f16,VEC,RS4>",
+            "kernel": "gather_gemm_staged<f16,f16,VEC>",
             "kernel_ms": round(kernel_ms, 5),
             "algorithmic_bytes": nbytes,
             "mfma_tflops": round(flops / (kernel_ms * 1e-3) / 1e12, 2),
