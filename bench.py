@@ -63,21 +63,24 @@ def gemm_bytes(n_in: int, n_out: int, plan_bytes: int) -> int:
 
 
 def plan_read_bytes(plan, kv: int, n_out: int) -> int:
-    """Bytes of the gather plan the staged kernel must read: per tile its
-    distinct-row list (4 B per row) and, per item, one uint16 LDS address per
-    output row (csrc/sp_plan.h layout)."""
+    """Bytes of the gather plan the staged kernel needs: per tile its
+    distinct-row list (4 B per row) and, per item of its groups of 4 items, one
+    uint16 LDS address per output row (csrc/sp_plan.h layout: 256-row tiles,
+    896 staged rows)."""
     import numpy as np
 
-    tile = 256
+    tile, lds_rows = 256, 896
     nt = (n_out + tile - 1) // tile
     buf = plan.cpu().numpy()
-    count = buf[256:256 + nt * 4].view(np.int32)
+    count = buf[256:256 + nt * 4].view(np.int32).astype(np.int64)
     align = lambda v: (v + 255) // 256 * 256
     ovf_off = align(256 + nt * 4)
     rows_off = align(ovf_off + nt * 4)
-    nact_off = align(rows_off + nt * 960 * 4)
-    nact = buf[nact_off:nact_off + nt * 4].view(np.int32)
-    return int(count.astype(np.int64).sum() * 4 + nact.astype(np.int64).sum() * tile * 2)
+    nact_off = align(rows_off + nt * lds_rows * 4)
+    nact = buf[nact_off:nact_off + nt * 4].view(np.int32).astype(np.int64)
+    staged = count < lds_rows
+    items = (nact + 3) // 4 * 4
+    return int((count[staged] * 4).sum() + (items[staged] * tile * 2).sum())
 
 
 def cpu_baseline(idx, feats_np, w_np, b_np, pf_np):

@@ -61,6 +61,7 @@ constexpr uint32_t kColOob = 0x40000000u;  // B column offset of columns >= N
 constexpr uint32_t kMaxBtBytes = 0x40000000u;  // packed weights must stay below (host check)
 constexpr int kGroupOffsets = 64;          // kernel offsets per group (direct kernel)
 constexpr uint32_t kSlabBytes = 4096;      // B of one item: 4 pieces x 64 columns x 16 B
+constexpr int kPad = 7;                    // padding items after a direct-kernel item list
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   // word 3 = 0x00020000: 32-bit data format, the raw-buffer setting for gfx9 parts
@@ -117,6 +118,14 @@ __device__ __forceinline__ int64_t xcd_tile(int64_t b, int64_t nb) {
 // B and A pipelines keep in flight across barriers).
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// The same with the wave's last `kPending` LDS operations still in flight
+// (LDS operations complete in order, so every earlier one is complete).
+template <int kPending>
+__device__ __forceinline__ void lds_barrier_pending() {
+  static_assert(kPending >= 0 && kPending < 16, "lgkmcnt holds 4 bits");
+  asm volatile("s_waitcnt lgkmcnt(%0)\n\ts_barrier" ::"n"(kPending) : "memory");
 }
 
 // Byte sizes of the buffers a launch touches; the host checks they fit in 32 bits.
@@ -414,10 +423,12 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_direct(
 // staged kernel
 // ---------------------------------------------------------------------------
 
-// Dynamic LDS of the staged kernel: B offsets of the tile's items, the byte
-// offsets of the tile's distinct rows in A, the staged rows (kLdsRows chunks)
-// and the B ring (3 slabs); the epilogue tiles overlap the staged rows and the
-// ring.
+constexpr int kRing = 4;  // B ring slots of the staged kernel (one item each)
+
+// Dynamic LDS of the staged kernel: B offsets of the tile's items (E plus the
+// read-ahead past the last group), the byte offsets of the tile's distinct rows
+// in A, the staged rows (kLdsRows chunks) and the B ring; the epilogue tiles
+// overlap the staged rows and the ring.
 struct StagedLds {
   uint32_t kb_off, rowoff_off, rows_off, ring_off, total;
 };
@@ -425,10 +436,10 @@ struct StagedLds {
 __host__ __device__ inline StagedLds staged_lds(int E, uint32_t out_size) {
   StagedLds l;
   l.kb_off = 0;
-  l.rowoff_off = (4u * uint32_t(E) + 255u) / 256u * 256u;
+  l.rowoff_off = (4u * uint32_t(E + 2 * kItemGroup) + 255u) / 256u * 256u;
   l.rows_off = l.rowoff_off + uint32_t(kLdsRows) * 4u;
   l.ring_off = l.rows_off + uint32_t(kLdsRows * kChunkBytes);
-  l.total = l.ring_off + 3u * kSlabBytes;
+  l.total = l.ring_off + uint32_t(kRing) * kSlabBytes;
   if (l.total < l.rows_off + epi_bytes(out_size)) l.total = l.rows_off + epi_bytes(out_size);
   return l;
 }
@@ -446,6 +457,7 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
   constexpr int kRowsPerLane = kLdsRows / 64;    // staged rows copied per thread and chunk
   static_assert(V * ES == 16, "fragments and B slab pieces are 16 bytes");
   static_assert(kLdsRows % 64 == 0, "rows are copied 64 per workgroup pass");
+  static_assert(kItemGroup == 4 && kRing == 4, "the step loop is unrolled over 4 items");
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int tid = threadIdx.x;
@@ -459,7 +471,7 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bt, nb.bt_bytes);
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(out, nb.out_bytes);
 
-  const int E = kv + kPad;
+  const int E = plan.E;
   const StagedLds L = staged_lds(E, uint32_t(sizeof(OutT)));
   uint32_t* s_kb = reinterpret_cast<uint32_t*>(smem + L.kb_off);
   unsigned char* rows_lds = smem + L.rows_off;
@@ -516,7 +528,10 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
         *reinterpret_cast<frag*>(smem + wbase + 4096u * uint32_t(j)) = st[j];
   };
   issue_stage(0);
-  if (tid < E) s_kb[tid] = ko >= 0 ? uint32_t(ko) * k_bytes : kBOob;
+  // B offsets of the items; the entries past the tile's items (padding and
+  // read-ahead) point past Bt, so their slabs read as zeros
+  if (tid < E + 2 * kItemGroup)
+    s_kb[tid] = (tid < E && ko >= 0) ? uint32_t(ko) * k_bytes : kBOob;
   floatx16 acc[2][2];
   zero_acc(acc);
   put_stage();
@@ -525,14 +540,23 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
   // this thread's 16-byte piece of every B slab: piece gp, column cp
   const int gp = tid >> 6, cp = n0 + (tid & 63);
   const uint32_t bpiece = cp < N ? uint32_t(cp) * V * ES : kColOob;
-  // this lane's 4-byte record of A addresses (rows l32 and 32 + l32 of its wave)
-  const uint32_t* arec = reinterpret_cast<const uint32_t*>(plan.addr + tile * E * kTileRows) +
-                         wave * 32 + l32;  // + item * 128 records
+  // this lane's 4-byte A address record of item i (rows l32 and 32 + l32 of
+  // its wave); items past the tile's last group read zeros (the staged row 0,
+  // whose fragments are never multiplied)
+  const int n_items = (nact + kItemGroup - 1) / kItemGroup * kItemGroup;
+  const __amdgpu_buffer_rsrc_t rrec =
+      make_rsrc(plan.addr + tile * E * kTileRows, uint32_t(E) * kTileRows * 2u);
+  const uint32_t rec_lane = uint32_t(wave) * 128u + uint32_t(l32) * 4u;
+  auto load_rec = [&](int i) -> uint32_t {
+    return __builtin_amdgcn_raw_buffer_load_b32(
+        rrec, i < n_items ? uint32_t(i) * 512u + rec_lane : kOob, 0, 0);
+  };
 
   for (int rc = 0; rc < nrc; ++rc) {
     const uint32_t bofs = uint32_t(rc * 4 + gp) * slab_bytes + bpiece;
     auto gload = [&](uint32_t kb) -> uint4 {  // this thread's piece of an item's B slab
-      return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rb, kb + bofs, 0, 0));
+      return __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(rb, kb + bofs, 0, 0));
     };
     auto ring_put = [&](int slot, const uint4& v) {
       *reinterpret_cast<uint4*>(ring + uint32_t(slot) * kSlabBytes + uint32_t(tid) * 16u) = v;
@@ -556,62 +580,84 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
                                                      (t2[mt] ^ (uint32_t(ks * 2 + h) << 4)));
     };
 
-    // ---- pipeline.  Item i's B slab is loaded from global memory in step
-    // i-4, written to ring slot i % 3 in step i-2, read into registers in
-    // step i-1; its A addresses are loaded in step i-3 and its A fragments
-    // read in step i-1; its MFMAs run in step i.  Step `it`:
-    //   1. ring write of item it+2 (the slot was last read two steps ago),
-    //      LDS reads of the A and B fragments of item it+1, B offset of it+4,
+    // ---- pipeline.  Item i's B piece is loaded from global memory in step
+    // i-6, written to ring slot i % 4 in step i-3 and read into registers in
+    // step i-1; its A address record is loaded in step i-5 and its A fragments
+    // are read in step i-1; its MFMAs run in step i.  Step `it`:
+    //   1. ring write of item it+3, LDS reads of item it+1's A and B
+    //      fragments, B offset of item it+6,
     //   2. the 8 MFMAs of item it (they cover the latency of the LDS work),
-    //   3. global loads of item it+4's B piece and item it+3's A addresses,
-    //   4. barrier (the ring slot written in 1 is read in the next step).
-    // Register rings of 3 (static indices, loop unrolled 3 times).
-    frag b0[2][2], b1[2][2], b2[2][2], a0[2][2], a1[2][2], a2[2][2];
-    uint4 q0, q1, q2;     // B pieces loaded, not yet in the ring
-    uint32_t r0, r1, r2;  // A address records
+    //   3. global loads of item it+6's B piece and item it+5's A record,
+    //   4. after odd steps, a barrier: a ring slot is written two steps after
+    //      its last read and read two steps after its write, so one barrier in
+    //      every two steps separates both.  The A reads are issued last and
+    //      the barrier leaves them in flight.
+    // The loop is unrolled over one group (4 steps), so every register and
+    // ring index is static.
+    frag fa[2][2][2], fb[2][2][2];  // [item parity][ks][mt or nt]
+    uint4 q[4];                     // B pieces loaded, not yet in the ring: item i in q[i % 4]
+    uint32_t r[4];                  // A address records: item i in r[i % 4]
     {
-      const uint32_t k0 = s_kb[0], k1 = s_kb[1], k2 = s_kb[2], k3 = s_kb[3];
-      const uint4 p0 = gload(k0), p1 = gload(k1);
-      r0 = arec[0];
-      r1 = arec[128];
-      r2 = arec[256];
-      q2 = gload(k2);
-      q0 = gload(k3);  // item 3 lives in register slot 3 % 3 = 0
-      // next chunk's rows: behind the B and A loads above, so the first items
-      // do not wait for them (past the last chunk the loads read zeros and are
-      // dropped)
-      issue_stage(rc + 1);
+      const uint4 p0 = gload(s_kb[0]), p1 = gload(s_kb[1]), p2 = gload(s_kb[2]);
+      r[0] = load_rec(0);
+      r[1] = load_rec(1);
+      r[2] = load_rec(2);
+      r[3] = load_rec(3);
+      q[3] = gload(s_kb[3]);
+      q[0] = gload(s_kb[4]);
+      q[1] = gload(s_kb[5]);
       ring_put(0, p0);
       ring_put(1, p1);
+      ring_put(2, p2);
       lds_barrier();
-      read_b(0, b0);
-      read_a(r0, a0);
+      read_b(0, fb[0]);
+      read_a(r[0], fa[0]);
+      r[0] = load_rec(4);
+      lds_barrier();  // the prologue counts as an odd step (slot 0 is rewritten in step 1)
     }
-    int kb_next = 0;
-    auto step = [&](int it, frag (&bc)[2][2], frag (&bn)[2][2], frag (&ac)[2][2],
-                    frag (&an)[2][2], uint32_t rn, uint32_t& r3, const uint4& q2s, uint4& q4) {
-      ring_put((it + 2) % 3, q2s);
-      read_b((it + 1) % 3, bn);
-      read_a(rn, an);
-      kb_next = s_kb[it + 4];
+    auto step = [&](int it, auto jc) {
+      constexpr int j = decltype(jc)::value;  // it % 4
+      ring_put((j + 3) % 4, q[(j + 3) % 4]);
+      read_b((j + 1) % 4, fb[(j + 1) % 2]);
+      const uint32_t kb = s_kb[it + 6];
       __builtin_amdgcn_sched_barrier(0);
-      mma_item<T>(ac, bc, acc);
+      read_a(r[(j + 1) % 4], fa[(j + 1) % 2]);  // last: the barrier does not wait for them
       __builtin_amdgcn_sched_barrier(0);
-      q4 = gload(uint32_t(kb_next));
-      r3 = arec[(it + 3) * 128];
+      mma_item<T>(fa[j % 2], fb[j % 2], acc);
       __builtin_amdgcn_sched_barrier(0);
-      lds_barrier();
+      q[(j + 2) % 4] = gload(kb);
+      r[(j + 1) % 4] = load_rec(it + 5);
+      __builtin_amdgcn_sched_barrier(0);
+      // the ring write and the B reads must be complete (the ring slots are
+      // shared); the four A reads of the rows, which no one rewrites during the
+      // chunk, stay in flight
+      if constexpr (j % 2 == 1) lds_barrier_pending<4>();
     };
-    // register slots: A records of item i in r[i % 3], B pieces of item i in
-    // q[i % 3]; item it+4 reuses the slot of item it+1 (already in the ring)
-    step(0, b0, b1, a0, a1, r1, r0, q2, q1);
-    step(1, b1, b2, a1, a2, r2, r1, q0, q2);
-    step(2, b2, b0, a2, a0, r0, r2, q1, q0);
-    for (int it = 3; it < nact; it += 3) {  // reads items up to max(nact + 5, 6) < nact + kPad
-      step(it, b0, b1, a0, a1, r1, r0, q2, q1);
-      step(it + 1, b1, b2, a1, a2, r2, r1, q0, q2);
-      step(it + 2, b2, b0, a2, a0, r0, r2, q1, q0);
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    step(0, I0{});
+    step(1, I1{});
+    // next chunk's rows: issued after the first steps' loads, so the waits of
+    // the next steps do not cover them (past the last chunk the loads read
+    // zeros and are dropped)
+    issue_stage(rc + 1);
+    step(2, I2{});
+    step(3, I3{});
+    for (int it = 4; it < n_items; it += kItemGroup) {
+      step(it, I0{});
+      step(it + 1, I1{});
+      step(it + 2, I2{});
+      step(it + 3, I3{});
     }
+    // The loads in flight are read here on every path, so that the compiler
+    // cannot sink the ones issued before the loop (only the loop reads them)
+    // to the loop's entry, which would issue them late.
+    using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
+    asm volatile("" ::"v"(__builtin_bit_cast(u32x4, q[0])), "v"(__builtin_bit_cast(u32x4, q[1])),
+                 "v"(__builtin_bit_cast(u32x4, q[2])), "v"(__builtin_bit_cast(u32x4, q[3])),
+                 "v"(r[0]), "v"(r[1]), "v"(r[2]), "v"(r[3]));
     if (rc + 1 < nrc) {
       put_stage();  // every wave is past the last barrier of chunk rc
       __syncthreads();

@@ -26,6 +26,8 @@
 // and read back as 16-byte MFMA operands.  The pair list of each offset is cut
 // into `splits` contiguous ranges whose fp32 partials are summed in a fixed
 // order by a second kernel (deterministic, no atomics).
+#include <type_traits>
+
 #include "sp_common.h"
 #include "sp_plan.h"
 
@@ -326,11 +328,11 @@ static int launch_direct(dim3 grid, hipStream_t s, const T* A, const T* bt, cons
 template <typename T, typename OutT, bool VEC>
 static int launch_staged(dim3 grid, hipStream_t s, const T* A, const T* bt, OutT* o, GemmBufs nb,
                          const GemmCall& c) {
-  const uint32_t lds = staged_lds(c.kv + kPad, uint32_t(sizeof(OutT))).total;
+  const uint32_t lds = staged_lds(c.plan.E, uint32_t(sizeof(OutT))).total;
   auto kern = gather_gemm_staged<T, OutT, VEC>;
   static bool attr_set = false;
   int rc = allow_lds(reinterpret_cast<const void*>(kern),
-                     staged_lds(kPlanMaxKv + kPad, uint32_t(sizeof(OutT))).total, attr_set);
+                     staged_lds(kPlanMaxKv, uint32_t(sizeof(OutT))).total, attr_set);
   if (rc) return rc;
   kern<<<grid, 256, lds, s>>>(A, bt, c.plan, c.bias, o, nb, c.M, c.N, c.R, c.Rp, c.kv);
   SP_LAUNCHED();

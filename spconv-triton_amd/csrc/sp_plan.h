@@ -10,34 +10,38 @@
 // there.  A plan holds what it needs for that, computed once per table:
 //   * per tile: U and the ascending list of distinct source rows;
 //   * per tile: the offsets with at least one pair among its rows ("items",
-//     ascending) followed by kPad padding items;
+//     ascending), which the GEMM takes in groups of kItemGroup;
 //   * for every (item, row) the LDS byte address of the row's staged chunk
 //     (chunk_base(slot); the zero row for a row without a pair, a row past M
-//     and every padding item).
+//     and the items that fill up the tile's last group).
 //
-// Layout of one plan buffer (256-byte aligned parts), E = kv + kPad:
+// Layout of one plan buffer (256-byte aligned parts), E = kv rounded up to a
+// multiple of kItemGroup:
 //   n_overflow                  int32   number of overflow tiles (below)
 //   count[ntiles]               int32   U of the tile; U >= kLdsRows marks an
 //                                       overflow tile, whose rows do not fit in
 //                                       LDS (nothing else is written for it)
 //   overflow[ntiles]            int32   ascending ids of the overflow tiles
 //   rows[ntiles][kLdsRows]      int32   ascending distinct source rows, then -1
-//   nact[ntiles]                int32   items of the tile (without padding)
-//   koff[ntiles][E]             int32   kernel offset of each item (-1: padding)
+//   nact[ntiles]                int32   items of the tile
+//   koff[ntiles][E]             int32   kernel offset of each item, then -1
 //   addr[ntiles][E][4][32][2]   uint16  for item i and wave w, the address of
 //                                       row w * 64 + mt * 32 + l32 of the tile,
 //                                       stored at [i][w][l32][mt] (one 128-byte
 //                                       record per wave and item; lane l of the
-//                                       wave reads the 4 bytes at l % 32)
+//                                       wave reads the 4 bytes at l % 32); the
+//                                       items that fill up the last group are
+//                                       written, later ones are not
+
 #pragma once
 #include "sp_common.h"
 
 namespace sp {
 
 constexpr int kTileRows = 256;      // output rows per GEMM workgroup (4 waves x 64)
-constexpr int kLdsRows = 960;       // staged rows per tile, including one zero row
+constexpr int kLdsRows = 896;       // staged rows per tile, including one zero row
 constexpr int kPlanMaxKv = 64;      // kTileRows * 64 = 16384 entries sorted in LDS
-constexpr int kPad = 7;             // padding items after the live ones (GEMM read-ahead)
+constexpr int kItemGroup = 4;       // the GEMM runs whole groups of items
 constexpr int kChunkBytes = 64;     // one MFMA K-step of one row (32 f16/bf16 or 16 f32)
 constexpr int kSwizzleShift = 2;    // piece p of a row sits at piece p ^ ((slot >> 2) & 3)
 
@@ -62,7 +66,7 @@ inline PlanLayout plan_layout(int64_t M, int64_t kv) {
   PlanLayout p;
   const int64_t m = M > 0 ? M : 1;
   p.ntiles = cdiv(m, kTileRows);
-  p.E = int(kv) + kPad;
+  p.E = int((kv + kItemGroup - 1) / kItemGroup * kItemGroup);
   const size_t nt = size_t(p.ntiles);
   p.count_off = 256;
   p.overflow_off = align_up(p.count_off + nt * 4, 256);

@@ -1,15 +1,25 @@
 // Gather-plan builder (layout and purpose in sp_plan.h).
 //
-// One workgroup per tile of kTileRows output rows: the tile's kTileRows * kv
-// entries are sorted in LDS with a bitonic network (no pair = INT32_MAX sorts
-// last), the distinct values are compacted in place, the tile's items are
-// numbered, and every entry's slot is found by binary search in the compacted
-// list and stored as its staged LDS address.  A second, single-workgroup
-// kernel lists the tiles whose rows do not fit in LDS; their number is copied
-// back to the host (the build's one synchronisation), so that a GEMM launches
-// the direct-gather kernel for them only when there are any.  The plan depends
-// only on the table, so the caller builds it once per table and reuses it for
-// every GEMM on that table.
+// One workgroup per tile of kTileRows output rows.  The tile's kTileRows * kv
+// entries are read once into registers (thread t holds entries i * 512 + t,
+// so the loads are coalesced along the rows).  The distinct valid entries are
+// then found in one of two ways:
+//   * bitmap (the usual case): the entries of a tile of a locality-ordered
+//     table fall in a narrow window [lo, hi] of source rows.  When the window
+//     fits in a bitmap in LDS, every entry sets its bit, a block scan of the
+//     words' popcounts gives every word's rank offset, and the rank of a row
+//     is that offset plus the popcount of the lower bits of its word: O(n)
+//     work with no sort;
+//   * sort (any table): the entries are sorted in LDS with a bitonic network
+//     (no pair = INT32_MAX sorts last), the distinct values are compacted in
+//     place, and every entry's rank is found by binary search.
+// Both give U and the ascending distinct list; the tile's items are numbered
+// and every (item, row) gets the staged LDS address of its rank.  A second,
+// single-workgroup kernel lists the tiles whose rows do not fit in LDS; their
+// number is copied back to the host (the build's one synchronisation), so
+// that a GEMM launches the direct-gather kernel for them only when there are
+// any.  The plan depends only on the table, so the caller builds it once per
+// table and reuses it for every GEMM on that table.
 #include "sp_plan.h"
 
 namespace sp {
@@ -21,83 +31,154 @@ __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
     const int32_t* __restrict__ pairs, int64_t M, int kv, int64_t n_src,
     int32_t* __restrict__ count, int32_t* __restrict__ rows_out, int32_t* __restrict__ nact_out,
     int32_t* __restrict__ koff_out, uint16_t* __restrict__ addr_out, int E) {
+  // sort path: the entries; bitmap path: NP / 2 bitmap words, then NP / 2
+  // word rank offsets
   __shared__ int32_t keys[NP];
   __shared__ uint32_t scan_lds[kPlanThreads / 64 + 1];
   __shared__ int32_t s_item[kPlanMaxKv];  // item number of offset k in the tile, or -1
+  __shared__ int32_t s_red[2][kPlanThreads / 64];
   __shared__ int32_t s_nact;
   constexpr int PER = NP / kPlanThreads;
   static_assert(PER <= 32, "first-occurrence flags are kept in one 32-bit mask");
   constexpr int32_t kNone = 0x7fffffff;
+  constexpr int kBmWords = NP / 2;
+  const int tid = threadIdx.x;
   const int64_t tile = blockIdx.x;
   const int64_t r0 = tile * kTileRows;
   const int n_ent = kTileRows * kv;
-  for (int e = threadIdx.x; e < NP; e += kPlanThreads) {
+
+  if (tid < kPlanMaxKv) s_item[tid] = -1;
+  __syncthreads();
+  // ---- entries into registers; window and items
+  int32_t v[PER];
+  int32_t lo = kNone, hi = -1;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = i * kPlanThreads + tid;
     int32_t key = kNone;
     if (e < n_ent) {
       const int k = e / kTileRows;
       const int64_t r = r0 + (e - k * kTileRows);
       if (r < M) {
-        const int32_t v = pairs[int64_t(k) * M + r];
-        if (v >= 0 && v < n_src) key = v;
-      }
-    }
-    keys[e] = key;
-  }
-  __syncthreads();
-  for (int size = 2; size <= NP; size <<= 1) {
-    for (int half = size >> 1; half > 0; half >>= 1) {
-      for (int i = threadIdx.x; i < NP / 2; i += kPlanThreads) {
-        const int lo = 2 * i - (i & (half - 1));
-        const int hi = lo + half;
-        const bool up = (lo & size) == 0;
-        const int32_t a = keys[lo], b = keys[hi];
-        if ((a > b) == up) {
-          keys[lo] = b;
-          keys[hi] = a;
+        const int32_t x = pairs[int64_t(k) * M + r];
+        if (x >= 0 && x < n_src) {
+          key = x;
+          s_item[k] = 0;  // every writer stores the same value
         }
       }
-      __syncthreads();
+    }
+    v[i] = key;
+    if (key != kNone) {
+      lo = key < lo ? key : lo;
+      hi = key > hi ? key : hi;
     }
   }
-  // first occurrences of valid values; thread t owns entries [t*PER, (t+1)*PER)
-  const int base = threadIdx.x * PER;
-  int32_t v[PER];
-  int32_t prev = base > 0 ? keys[base - 1] : kNone;
-  uint32_t firsts = 0;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    v[i] = keys[base + i];
-    if (v[i] != kNone && v[i] != prev) firsts |= 1u << i;
-    prev = v[i];
+  for (int off = 32; off > 0; off >>= 1) {
+    const int32_t ol = __shfl_xor(lo, off, 64), oh = __shfl_xor(hi, off, 64);
+    lo = ol < lo ? ol : lo;
+    hi = oh > hi ? oh : hi;
   }
-  uint32_t total = 0;
-  uint32_t pos = block_exclusive_scan<kPlanThreads>(uint32_t(__builtin_popcount(firsts)),
-                                                    scan_lds, &total);
-  __syncthreads();  // all entries read: compact in place (pos <= entry index)
-#pragma unroll
-  for (int i = 0; i < PER; ++i)
-    if (firsts & (1u << i)) keys[pos++] = v[i];
+  if ((tid & 63) == 0) {
+    s_red[0][tid >> 6] = lo;
+    s_red[1][tid >> 6] = hi;
+  }
   __syncthreads();
-  const int U = int(total);
-  if (threadIdx.x == 0) count[tile] = U;
+  lo = kNone;
+  hi = -1;
+#pragma unroll
+  for (int w = 0; w < kPlanThreads / 64; ++w) {
+    lo = s_red[0][w] < lo ? s_red[0][w] : lo;
+    hi = s_red[1][w] > hi ? s_red[1][w] : hi;
+  }
+  const int64_t window = hi >= 0 ? int64_t(hi) - lo + 1 : 0;
+  const bool use_bitmap = window <= int64_t(kBmWords) * 32;
+  uint32_t* bm = reinterpret_cast<uint32_t*>(keys);
+  uint32_t* pre = bm + kBmWords;
+  int32_t* rows_t = rows_out + tile * kLdsRows;
+  int U;
+  if (use_bitmap) {
+    const int nw = int((window + 31) / 32);
+    for (int w = tid; w < nw; w += kPlanThreads) bm[w] = 0u;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (v[i] != kNone) {
+        const uint32_t d = uint32_t(v[i] - lo);
+        atomicOr(&bm[d >> 5], 1u << (d & 31));
+      }
+    __syncthreads();
+    // thread t ranks words [t * wpt, (t + 1) * wpt)
+    const int wpt = (nw + kPlanThreads - 1) / kPlanThreads;
+    const int w0 = tid * wpt, w1 = w0 + wpt < nw ? w0 + wpt : nw;
+    uint32_t cnt = 0;
+    for (int w = w0; w < w1; ++w) cnt += uint32_t(__builtin_popcount(bm[w]));
+    uint32_t total = 0;
+    uint32_t pos = block_exclusive_scan<kPlanThreads>(cnt, scan_lds, &total);
+    U = int(total);
+    for (int w = w0; w < w1; ++w) {
+      pre[w] = pos;
+      uint32_t bits = bm[w];
+      if (U < kLdsRows)
+        while (bits) {
+          const int b = __builtin_ctz(bits);
+          bits &= bits - 1;
+          rows_t[pos++] = lo + w * 32 + b;
+        }
+      else
+        pos += uint32_t(__builtin_popcount(bits));
+    }
+    __syncthreads();
+  } else {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) keys[i * kPlanThreads + tid] = v[i];
+    __syncthreads();
+    for (int size = 2; size <= NP; size <<= 1) {
+      for (int half = size >> 1; half > 0; half >>= 1) {
+        for (int i = tid; i < NP / 2; i += kPlanThreads) {
+          const int a = 2 * i - (i & (half - 1));
+          const int c = a + half;
+          const bool up = (a & size) == 0;
+          const int32_t x = keys[a], y = keys[c];
+          if ((x > y) == up) {
+            keys[a] = y;
+            keys[c] = x;
+          }
+        }
+        __syncthreads();
+      }
+    }
+    // first occurrences of valid values; thread t owns entries [t*PER, (t+1)*PER)
+    const int base = tid * PER;
+    int32_t sv[PER];
+    int32_t prev = base > 0 ? keys[base - 1] : kNone;
+    uint32_t firsts = 0;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      sv[i] = keys[base + i];
+      if (sv[i] != kNone && sv[i] != prev) firsts |= 1u << i;
+      prev = sv[i];
+    }
+    uint32_t total = 0;
+    uint32_t pos = block_exclusive_scan<kPlanThreads>(uint32_t(__builtin_popcount(firsts)),
+                                                      scan_lds, &total);
+    __syncthreads();  // all entries read: compact in place (pos <= entry index)
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (firsts & (1u << i)) keys[pos++] = sv[i];
+    __syncthreads();
+    U = int(total);
+    if (U < kLdsRows)
+      for (int i = tid; i < U; i += kPlanThreads) rows_t[i] = keys[i];
+  }
+  if (tid == 0) count[tile] = U;
   if (U >= kLdsRows) return;  // the GEMM gathers this tile straight from memory
   // the list is padded with -1 to kLdsRows entries, so that the GEMM can load
   // it without waiting for the count
-  for (int i = threadIdx.x; i < kLdsRows; i += kPlanThreads)
-    rows_out[tile * kLdsRows + i] = i < U ? keys[i] : -1;
+  for (int i = U + tid; i < kLdsRows; i += kPlanThreads) rows_t[i] = -1;
 
   // items of the tile: the offsets with a pair among its rows
-  for (int i = threadIdx.x; i < kPlanMaxKv; i += kPlanThreads) s_item[i] = -1;
-  __syncthreads();
-  for (int e = threadIdx.x; e < n_ent; e += kPlanThreads) {
-    const int k = e / kTileRows, lr = e - k * kTileRows;
-    const int64_t r = r0 + lr;
-    if (r >= M) continue;
-    const int32_t x = pairs[int64_t(k) * M + r];
-    if (x >= 0 && x < n_src) s_item[k] = 0;  // every writer stores the same value
-  }
-  __syncthreads();
-  if (threadIdx.x == 0) {
+  if (tid == 0) {
     int32_t* ko = koff_out + tile * E;
     int n = 0;
     for (int k = 0; k < kv; ++k)
@@ -105,39 +186,50 @@ __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
         s_item[k] = n;
         ko[n++] = k;
       }
-    for (int q = 0; q < kPad; ++q) ko[n + q] = -1;
+    for (int q = n; q < E; ++q) ko[q] = -1;
     s_nact = n;
     nact_out[tile] = n;
   }
   __syncthreads();
-  // LDS address of every (item, row): the row's slot, found by binary search
-  // in the distinct list, or the zero row
+  // LDS address of every (item, row): the staged slot of the row's rank, or
+  // the zero row
   const uint16_t zero = uint16_t(chunk_base(uint32_t(U)));
   uint16_t* at = addr_out + tile * E * kTileRows;
-  for (int e = threadIdx.x; e < n_ent; e += kPlanThreads) {
+  auto rec = [&](int item, int lr) -> uint16_t& {  // [item][wave][l32][mt]
+    const int w = lr / 64, ml = lr % 64;
+    return at[((item * 4 + w) * 32 + (ml % 32)) * 2 + ml / 32];
+  };
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int e = i * kPlanThreads + tid;
+    if (e >= n_ent) continue;
     const int k = e / kTileRows, lr = e - k * kTileRows;
     const int item = s_item[k];
     if (item < 0) continue;
-    const int64_t r = r0 + lr;
     uint16_t a = zero;
-    const int32_t x = r < M ? pairs[int64_t(k) * M + r] : -1;
-    if (x >= 0 && x < n_src) {
-      int lo = 0, hi = U;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (keys[mid] < x) lo = mid + 1;
-        else hi = mid;
+    const int32_t x = v[i];
+    if (x != kNone) {
+      int rank;
+      if (use_bitmap) {
+        const uint32_t d = uint32_t(x - lo);
+        rank = int(pre[d >> 5]) + __builtin_popcount(bm[d >> 5] & ((1u << (d & 31)) - 1u));
+      } else {
+        int l = 0, h = U;
+        while (l < h) {
+          const int mid = (l + h) >> 1;
+          if (keys[mid] < x) l = mid + 1;
+          else h = mid;
+        }
+        rank = l;
       }
-      a = uint16_t(chunk_base(uint32_t(lo)));
+      a = uint16_t(chunk_base(uint32_t(rank)));
     }
-    const int w = lr / 64, ml = lr % 64;
-    at[((item * 4 + w) * 32 + (ml % 32)) * 2 + ml / 32] = a;
+    rec(item, lr) = a;
   }
-  // padding items: every row reads the zero row
-  for (int i = threadIdx.x; i < kPad * kTileRows; i += kPlanThreads) {
-    const int q = i / kTileRows, lr = i % kTileRows, w = lr / 64, ml = lr % 64;
-    at[(((s_nact + q) * 4 + w) * 32 + (ml % 32)) * 2 + ml / 32] = zero;
-  }
+  // the items that fill up the last group read the zero row
+  const int n_fill = (kItemGroup - s_nact % kItemGroup) % kItemGroup;
+  for (int i = tid; i < n_fill * kTileRows; i += kPlanThreads)
+    rec(s_nact + i / kTileRows, i % kTileRows) = zero;
 }
 
 // Single workgroup: ascending list of the overflow tiles and their number.

@@ -21,8 +21,8 @@ pytestmark = pytest.mark.gpu
 
 DEV = "cuda:0"
 TILE = 256
-LDS_ROWS = 960  # kLdsRows of csrc/sp_plan.h
-PAD = 7  # kPad of csrc/sp_plan.h
+LDS_ROWS = 896  # kLdsRows of csrc/sp_plan.h
+GROUP = 4  # kItemGroup of csrc/sp_plan.h
 
 
 def _align(v, a=256):
@@ -38,7 +38,7 @@ def _chunk_base(slot):
 def _parse(plan, kv, M):
     """Split a plan buffer into its parts (layout of csrc/sp_plan.h)."""
     nt = (max(M, 1) + TILE - 1) // TILE
-    E = kv + PAD
+    E = (kv + GROUP - 1) // GROUP * GROUP
     buf = plan.cpu().numpy()
     count_off = 256
     ovf_off = _align(count_off + nt * 4)
@@ -62,9 +62,9 @@ def _parse(plan, kv, M):
 
 def _check_plan(pf, n_src):
     """Every part of the plan against numpy: per tile np.unique of the valid
-    sources, the offsets with a pair (ascending) then padding, and per (item,
-    row) the staged address of the row's rank in the unique list
-    (np.searchsorted), or of the zero row U."""
+    sources, the offsets with a pair (ascending) then -1, and per (item, row)
+    the staged address of the row's rank in the unique list (np.searchsorted),
+    or of the zero row U, up to the end of the tile's last group of items."""
     from spconv_triton.pytorch._impl import gemm
 
     kv, M = pf.shape
@@ -91,11 +91,12 @@ def _check_plan(pf, n_src):
         n = live.size
         assert P["nact"][t] == n, f"tile {t}: {P['nact'][t]} items != {n}"
         np.testing.assert_array_equal(P["koff"][t, :n], live)
-        assert (P["koff"][t, n:n + PAD] == -1).all()
-        exp = np.full((n + PAD, TILE), _chunk_base(U), dtype=np.int64)
+        assert (P["koff"][t, n:] == -1).all()
+        n4 = (n + GROUP - 1) // GROUP * GROUP
+        exp = np.full((n4, TILE), _chunk_base(U), dtype=np.int64)
         a = addr[live]
         exp[:n, :a.shape[1]] = a  # rows past M (last tile) keep the zero row
-        np.testing.assert_array_equal(P["addr"][t, :n + PAD].astype(np.int64), exp)
+        np.testing.assert_array_equal(P["addr"][t, :n4].astype(np.int64), exp)
     assert n_over_host == P["n_ovf"] == len(overflow)
     np.testing.assert_array_equal(P["ovf"], np.asarray(overflow, dtype=np.int32))
     return len(overflow)
@@ -117,7 +118,7 @@ def test_plan_layout_limits():
 
 
 @pytest.mark.parametrize("case", ["subm", "strided_fwd", "strided_bwd", "tiny", "exact_tiles",
-                                  "overflow", "kv64"])
+                                  "overflow", "kv64", "wide_window", "empty_rows"])
 def test_plan_matches_numpy(case):
     rng = np.random.default_rng(7)
     if case in ("subm", "strided_fwd", "strided_bwd"):
@@ -135,6 +136,16 @@ def test_plan_matches_numpy(case):
         pf, n_src = _random_table(rng, 27, 512, 800, 0.3), 800
     elif case == "overflow":
         pf, n_src = _random_table(rng, 27, 700, 100_000, 0.7), 100_000
+    elif case == "wide_window":
+        # sources spread over 5M rows: too wide a window for the bitmap, so the
+        # builder sorts
+        pf, n_src = _random_table(rng, 27, 600, 5_000_000, 0.05), 5_000_000
+    elif case == "empty_rows":
+        # tiles without any pair, and out-of-range sources (ignored)
+        t = rng.integers(0, 2000, size=(8, 900)).astype(np.int32)
+        t[:, 256:600] = -1
+        t[0, 700:710] = 5000
+        pf, n_src = torch.from_numpy(t).to(DEV), 2000
     else:
         pf, n_src = _random_table(rng, 64, 600, 900, 0.2), 900
     n_over = _check_plan(pf.contiguous(), n_src)
@@ -182,8 +193,8 @@ def test_planned_equals_unplanned(ci, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
 def test_planned_overflow_tiles(dtype):
-    """Tiles with >= 1023 distinct rows take the direct gather inside the planned
-    kernel; mixed with staged tiles the result must not change."""
+    """Tiles with too many distinct rows for LDS are left to the direct kernel;
+    mixed with staged tiles the result must not change."""
     rng = np.random.default_rng(11)
     kv, M, n_src, C, K = 27, 1500, 50_000, 32, 64
     t = rng.integers(0, n_src, size=(kv, M)).astype(np.int32)
