@@ -584,14 +584,13 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
     // i-6, written to ring slot i % 4 in step i-3 and read into registers in
     // step i-1; its A address record is loaded in step i-5 and its A fragments
     // are read in step i-1; its MFMAs run in step i.  Step `it`:
-    //   1. ring write of item it+3, LDS reads of item it+1's A and B
-    //      fragments, B offset of item it+6,
-    //   2. the 8 MFMAs of item it (they cover the latency of the LDS work),
-    //   3. global loads of item it+6's B piece and item it+5's A record,
-    //   4. after odd steps, a barrier: a ring slot is written two steps after
+    //   1. ring write of item it+3,
+    //   2. the 8 MFMAs of item it, and between them the LDS reads of item
+    //      it+1's A and B fragments, the B offset of item it+6, and the global
+    //      loads of item it+5's A record and item it+6's B piece,
+    //   3. after odd steps, a barrier: a ring slot is written two steps after
     //      its last read and read two steps after its write, so one barrier in
-    //      every two steps separates both.  The A reads are issued last and
-    //      the barrier leaves them in flight.
+    //      every two steps separates both.
     // The loop is unrolled over one group (4 steps), so every register and
     // ring index is static.
     frag fa[2][2][2], fb[2][2][2];  // [item parity][ks][mt or nt]
@@ -615,23 +614,66 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
       r[0] = load_rec(4);
       lds_barrier();  // the prologue counts as an odd step (slot 0 is rewritten in step 1)
     }
+    // One MFMA at a time with the step's other work between them: a wave
+    // that issues its eight MFMAs back to back waits for the MFMA pipe (which
+    // it shares with the other workgroup's wave on its SIMD) and then does its
+    // LDS, global and barrier work while the pipe idles; interleaved, that
+    // work is issued in the shadow of the MFMAs.
     auto step = [&](int it, auto jc) {
       constexpr int j = decltype(jc)::value;  // it % 4
-      ring_put((j + 3) % 4, q[(j + 3) % 4]);
-      read_b((j + 1) % 4, fb[(j + 1) % 2]);
+      const frag(&ac)[2][2] = fa[j % 2];
+      const frag(&bc)[2][2] = fb[j % 2];
+      frag(&an)[2][2] = fa[(j + 1) % 2];
+      frag(&bn)[2][2] = fb[(j + 1) % 2];
+      const uint32_t e = r[(j + 1) % 4];
+      const uint32_t t2[2] = {e & 0xffffu, e >> 16};
+      const unsigned char* slot_b = ring + uint32_t((j + 1) % 4) * kSlabBytes;
+      auto rd_a = [&](int ks, int mt) {
+        an[ks][mt] = *reinterpret_cast<const frag*>(rows_lds +
+                                                   (t2[mt] ^ (uint32_t(ks * 2 + h) << 4)));
+      };
+      auto rd_b = [&](int ks, int nt) {
+        bn[ks][nt] = *reinterpret_cast<const frag*>(slot_b + uint32_t(ks * 2 + h) * 1024u +
+                                                   uint32_t(nt * 32 + l32) * 16u);
+      };
+      auto mma = [&](int ks, int mt, int nt) {
+        Mfma<T>::mma(ac[ks][mt], bc[ks][nt], acc[mt][nt]);
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      // first LDS operation of the step: the B load below waits for it, and
+      // LDS operations complete in order, so issued last it would make that
+      // wait drain every fragment read of the step
       const uint32_t kb = s_kb[it + 6];
+      ring_put((j + 3) % 4, q[(j + 3) % 4]);
       __builtin_amdgcn_sched_barrier(0);
-      read_a(r[(j + 1) % 4], fa[(j + 1) % 2]);  // last: the barrier does not wait for them
+      // fragment reads in the order the next step's MFMAs consume them
+      mma(0, 0, 0);
+      rd_a(0, 0);
+      rd_b(0, 0);
       __builtin_amdgcn_sched_barrier(0);
-      mma_item<T>(fa[j % 2], fb[j % 2], acc);
+      mma(0, 0, 1);
+      rd_b(0, 1);
+      rd_a(0, 1);
       __builtin_amdgcn_sched_barrier(0);
-      q[(j + 2) % 4] = gload(kb);
+      mma(0, 1, 0);
+      rd_a(1, 0);
+      rd_b(1, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(0, 1, 1);
+      rd_b(1, 1);
+      rd_a(1, 1);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(1, 0, 0);
+      mma(1, 0, 1);
       r[(j + 1) % 4] = load_rec(it + 5);
       __builtin_amdgcn_sched_barrier(0);
-      // the ring write and the B reads must be complete (the ring slots are
-      // shared); the four A reads of the rows, which no one rewrites during the
-      // chunk, stay in flight
-      if constexpr (j % 2 == 1) lds_barrier_pending<4>();
+      mma(1, 1, 0);
+      q[(j + 2) % 4] = gload(kb);
+      __builtin_amdgcn_sched_barrier(0);
+      mma(1, 1, 1);
+      // the ring write and the B reads must be complete before the barrier
+      // (the ring slots are shared)
+      if constexpr (j % 2 == 1) lds_barrier();
     };
     using I0 = std::integral_constant<int, 0>;
     using I1 = std::integral_constant<int, 1>;
