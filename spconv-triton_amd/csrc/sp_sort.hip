@@ -4,7 +4,12 @@
 // consecutive items, visited in 8 rounds; in round r wave w holds items
 // [r*256 + w*64, +64).  The 32 (round, wave) segments are in item order, so a
 // per-digit exclusive scan over them plus the in-wave peer rank gives a stable
-// local rank.  Global placement: exclusive scan over hist[digit][tile].
+// local rank.  Global placement of digit d of tile b: all items with a smaller
+// digit plus the items of digit d in tiles before b.  Up to kRsFusedTiles
+// tiles, the histograms are stored tile-major and every scatter workgroup
+// sums them itself (one coalesced 1 KiB row per tile, then a 256-wide block
+// scan), so a pass is two launches; above that they are stored digit-major and
+// a device-wide exclusive scan gives the placements.
 #include "sp_sort.h"
 
 namespace sp {
@@ -14,6 +19,7 @@ constexpr int kRsRounds = 8;
 constexpr int kRsTile = kRsThreads * kRsRounds;  // 2048
 constexpr int kRsRadix = 256;
 constexpr int kRsSegs = kRsRounds * (kRsThreads / 64);  // 32
+constexpr int64_t kRsFusedTiles = 128;  // per scatter workgroup: 128 KiB of histogram reads
 
 struct RowWordDigit {
   const uint32_t* words;
@@ -68,7 +74,36 @@ __global__ __launch_bounds__(kRsThreads) void rs_hist(const Item* __restrict__ i
     if (valid && (peers & lanemask_lt()) == 0) atomicAdd(&cnt[d], uint32_t(__popcll(peers)));
   }
   __syncthreads();
-  hist[int64_t(threadIdx.x) * ntiles + blockIdx.x] = cnt[threadIdx.x];
+  if (ntiles <= kRsFusedTiles)
+    hist[int64_t(blockIdx.x) * kRsRadix + threadIdx.x] = cnt[threadIdx.x];  // [tile][digit]
+  else
+    hist[int64_t(threadIdx.x) * ntiles + blockIdx.x] = cnt[threadIdx.x];  // [digit][tile]
+}
+
+// Placement of this tile's digits from tile-major histograms (thread d: digit d).
+__device__ __forceinline__ uint32_t fused_tile_base(const uint32_t* __restrict__ hist,
+                                                    int64_t ntiles, uint32_t* scan_lds) {
+  const uint32_t d = threadIdx.x;
+  const int64_t me = blockIdx.x;
+  uint32_t total = 0, pre = 0;
+  int64_t b = 0;
+  for (; b + 8 <= ntiles; b += 8) {
+    uint32_t h[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) h[u] = hist[(b + u) * kRsRadix + d];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      total += h[u];
+      pre += b + u < me ? h[u] : 0u;
+    }
+  }
+  for (; b < ntiles; ++b) {
+    const uint32_t h = hist[b * kRsRadix + d];
+    total += h;
+    pre += b < me ? h : 0u;
+  }
+  uint32_t all = 0;
+  return block_exclusive_scan<kRsThreads>(total, scan_lds, &all) + pre;
 }
 
 template <class Item, class Digit>
@@ -79,8 +114,12 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter(const Item* __restrict_
                                                         int64_t ntiles) {
   __shared__ uint32_t seg[kRsSegs][kRsRadix];
   __shared__ uint32_t tile_base[kRsRadix];
+  __shared__ uint32_t scan_lds[kRsThreads / 64 + 1];
   for (int i = threadIdx.x; i < kRsSegs * kRsRadix; i += kRsThreads) (&seg[0][0])[i] = 0;
-  tile_base[threadIdx.x] = offsets[int64_t(threadIdx.x) * ntiles + blockIdx.x];
+  if (ntiles <= kRsFusedTiles)
+    tile_base[threadIdx.x] = fused_tile_base(offsets, ntiles, scan_lds);
+  else
+    tile_base[threadIdx.x] = offsets[int64_t(threadIdx.x) * ntiles + blockIdx.x];
   __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t base = int64_t(blockIdx.x) * kRsTile;
@@ -139,8 +178,10 @@ static int radix_pass(const Item* in, Item* out, int64_t n, Digit dig, const RsB
   rs_hist<Item, Digit><<<dim3(unsigned(ntiles)), dim3(kRsThreads), 0, s>>>(in, n, dig, b.hist,
                                                                           ntiles);
   SP_LAUNCHED();
-  int rc = exclusive_scan_u32(b.hist, b.hist, int64_t(kRsRadix) * ntiles, nullptr, b.scan_ws, s);
-  if (rc) return rc;
+  if (ntiles > kRsFusedTiles) {
+    int rc = exclusive_scan_u32(b.hist, b.hist, int64_t(kRsRadix) * ntiles, nullptr, b.scan_ws, s);
+    if (rc) return rc;
+  }
   rs_scatter<Item, Digit><<<dim3(unsigned(ntiles)), dim3(kRsThreads), 0, s>>>(in, out, n, dig,
                                                                              b.hist, ntiles);
   SP_LAUNCHED();

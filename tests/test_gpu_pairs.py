@@ -289,3 +289,27 @@ def test_large_subm_properties():
     _eq(r2[3], exp[3], "pair_bwd 20k")
     _eq(r2[4][0], exp[4][0], "pair_mask 20k")
     _eq(r2[6][0], exp[6][0], "mask_argsort 20k")
+
+
+@pytest.mark.parametrize("n,grid", [(200_000, 256), (600_000, 512)])
+def test_mask_sort_stable_large(n, grid):
+    """The mask sort is a stable ascending sort of the mask words: at 200k rows
+    (98 radix tiles, placements summed inside the scatter) and 600k rows (293
+    tiles, device-wide scan of the histograms), mask_argsort equals numpy's
+    stable argsort of the words that the table's bits define."""
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+
+    from bench_data import surface_cloud
+
+    idx = surface_cloud(n, grid, seed=3)
+    t = torch.from_numpy(idx).to(DEV)
+    res = ops.get_indice_pairs_implicit_gemm(t, 1, [grid] * 3, ConvAlgo.MaskImplicitGemm,
+                                             [3] * 3, [1] * 3, [1] * 3, [1] * 3, [0] * 3, True,
+                                             is_train=False)
+    pf = res[2].cpu().numpy()
+    words = ((pf >= 0).astype(np.int64) << np.arange(27)[:, None]).sum(0)
+    exp = np.argsort(words, kind="stable")
+    np.testing.assert_array_equal(res[6][0].cpu().numpy(), exp)
+    np.testing.assert_array_equal(res[4][0][:, 0].cpu().numpy().astype(np.int64) & 0xFFFFFFFF,
+                                  words[exp])
