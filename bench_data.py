@@ -6,6 +6,8 @@
   1-3 % occupancy of a 256^3 grid at 200k voxels.
 * ``lidar_cloud``: ground plane with range fall-off plus random boxes in a
   [41, 1600, 1408] zyx grid (config 3).
+* ``urban_cloud``: road plane, building walls and object boxes in a
+  [128, 2048, 2048] zyx grid (config 4).
 
 Voxel rows are returned in ascending batch-major linear-key order, the order
 a voxeliser followed by a sort (or torch.unique) produces.  Indices are
@@ -100,6 +102,43 @@ def lidar_cloud(per_sample: int = 20000, batch: int = 4, seed: int = 0,
                 face[np.arange(4000), axis] = np.sign(face[np.arange(4000), axis]) * ext[axis] / 2
                 boxes.append(c + face)
             p = np.floor(np.concatenate([ground] + boxes, 0)).astype(np.int64)
+            p = p[((p >= 0) & (p < np.asarray(shape))).all(1)]
+            keys = np.unique(np.concatenate([keys, np.ravel_multi_index(p.T, shape)]))
+        pick = np.sort(rng.choice(keys.size, size=per_sample, replace=False))
+        out.append(keys[pick])
+    return _finish(out, list(shape))
+
+
+def urban_cloud(per_sample: int = 120000, batch: int = 2, seed: int = 0,
+                shape=(128, 2048, 2048)) -> np.ndarray:
+    """Road plane (z ~ 4-6), vertical building walls and object boxes."""
+    zdim, ydim, xdim = shape
+    out = []
+    for b in range(batch):
+        rng = np.random.default_rng(seed * 1000 + 500 + b)
+        keys = np.zeros(0, np.int64)
+        while keys.size < per_sample:
+            m = per_sample
+            road = np.stack([rng.uniform(4, 6, m), rng.uniform(0, ydim, m), rng.uniform(0, xdim, m)], 1)
+            parts = [road]
+            for _ in range(12):  # walls: vertical rectangles along y or x
+                length = rng.uniform(0.1, 0.5) * max(ydim, xdim)
+                height = rng.uniform(0.3, 0.9) * zdim
+                c = np.array([0.0, rng.uniform(0, ydim), rng.uniform(0, xdim)])
+                t = rng.uniform(-0.5, 0.5, m // 8) * length
+                z = rng.uniform(4, 4 + height, m // 8)
+                wall = np.stack([z, np.full_like(z, c[1]), c[2] + t], 1)
+                if rng.random() < 0.5:
+                    wall = np.stack([z, c[1] + t, np.full_like(z, c[2])], 1)
+                parts.append(wall)
+            for _ in range(40):  # objects: box surfaces standing on the road
+                ext = rng.uniform(0.01, 0.03, 3) * np.array([zdim * 4, ydim, xdim])
+                c = np.array([5 + ext[0] / 2, rng.uniform(0, ydim), rng.uniform(0, xdim)])
+                face = rng.uniform(-0.5, 0.5, (2000, 3)) * ext
+                axis = rng.integers(0, 3, 2000)
+                face[np.arange(2000), axis] = np.sign(face[np.arange(2000), axis]) * ext[axis] / 2
+                parts.append(c + face)
+            p = np.floor(np.concatenate(parts, 0)).astype(np.int64)
             p = p[((p >= 0) & (p < np.asarray(shape))).all(1)]
             keys = np.unique(np.concatenate([keys, np.ravel_multi_index(p.T, shape)]))
         pick = np.sort(rng.choice(keys.size, size=per_sample, replace=False))

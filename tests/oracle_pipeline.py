@@ -50,6 +50,29 @@ class OTensor:
         return OTensor(feats, self.indices, self.spatial_shape, self.batch_size, self.indice_dict)
 
 
+# Storage precision to emulate (None: plain fp64).  With torch.float16 the
+# oracle rounds every tensor that the GPU path stores in fp16 under
+# torch.autocast -- sparse-op inputs, weights and outputs, dense-glue outputs,
+# and the gradients flowing back through each of them -- while all arithmetic
+# stays fp64, so only accumulation order separates it from the GPU.
+ROUND = None
+
+
+class _RoundFn(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, dtype):
+        ctx.dtype = dtype
+        return x.to(dtype).to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, g):
+        return g.to(ctx.dtype).to(g.dtype), None
+
+
+def _r(x):
+    return x if ROUND is None else _RoundFn.apply(x, ROUND)
+
+
 class _GemmFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, feats, weight, pf, pb):
@@ -130,9 +153,10 @@ class OConv:
     def __call__(self, x: OTensor, training=True):
         feats = x.features
         if self.conv1x1:
-            out = feats @ self.weight.view(self.cin, self.cout)   # raw reinterpretation (conv.py:198-201)
+            # raw reinterpretation (conv.py:198-201)
+            out = _r(_r(feats) @ _r(self.weight).view(self.cin, self.cout))
             if self.bias is not None:
-                out = out + self.bias
+                out = _r(out + self.bias)
             return x.replace(out)
         indice_dict = dict(x.indice_dict)
         if self.inverse:
@@ -160,7 +184,7 @@ class OConv:
                 indice_dict[self.indice_key] = {"pair_fwd": pf, "pair_bwd": pb, "out_indices": outids,
                                                 "indices": x.indices, "spatial_shape": list(x.spatial_shape),
                                                 "out_spatial_shape": out_shape}
-        out = _GemmFn.apply(feats, self.weight, pf, pb)
+        out = _r(_GemmFn.apply(_r(feats), _r(self.weight), pf, pb))
         if self.bias is not None:
             out = out + self.bias
         return OTensor(out, outids, out_shape, x.batch_size, indice_dict)
@@ -176,6 +200,7 @@ class OPool:
         self.dilation = expand_nd(ndim, dilation)
         self.subm = subm
         self.is_max = is_max
+        self.indice_key = indice_key  # registered like a conv's (reference pool.py:152-201)
 
     def params(self):
         return {}
@@ -187,8 +212,14 @@ class OPool:
         out_shape = list(x.spatial_shape) if self.subm else orc.get_conv_output_size(
             x.spatial_shape, self.ksize, self.stride, self.padding, self.dilation)
         fn = _MaxPoolFn if self.is_max else _AvgPoolFn
-        out = fn.apply(x.features, pf, pb)
-        return OTensor(out, outids, out_shape, x.batch_size, dict(x.indice_dict))
+        out = _r(fn.apply(_r(x.features), pf, pb))
+        indice_dict = dict(x.indice_dict)
+        if self.indice_key is not None:
+            indice_dict[self.indice_key] = {"pair_fwd": pf, "pair_bwd": pb, "out_indices": outids,
+                                            "indices": x.indices,
+                                            "spatial_shape": list(x.spatial_shape),
+                                            "out_spatial_shape": out_shape}
+        return OTensor(out, outids, out_shape, x.batch_size, indice_dict)
 
 
 class ODense:
@@ -202,7 +233,7 @@ class ODense:
 
     def __call__(self, x: OTensor, training=True):
         self.mod.train(training)
-        return x.replace(self.mod(x.features))
+        return x.replace(_r(self.mod(x.features)))
 
 
 class OSeq:
