@@ -256,6 +256,68 @@ int sp_avgpool_bwd(const void* gout, const int32_t* count, int32_t dtype, int64_
                    int64_t C, const int32_t* pb, int64_t kv, int64_t n_in, void* dx,
                    void* stream);
 
+/* ---- point-cloud voxelisation ------------------------------------------ */
+
+/* Workspace bytes of sp_point2voxel (0 for bad sizes). */
+size_t sp_point2voxel_workspace_size(int64_t n_points, int64_t max_voxels);
+
+/* PointToVoxel.generate_voxel_with_id (spconv_triton/pytorch/utils.py:72-163).
+ * points [n_points, point_cols] f32 or f64 (dtype), the first ndim columns x,
+ * y, z, ...; a point's voxel is floor((p - coors_min) / vsize) per axis,
+ * computed in the points' precision, kept when inside grid_size_xyz.  Voxels
+ * are numbered in order of their first point, at most max_voxels of them;
+ * each stores up to max_points_per_voxel points (num_point_features columns,
+ * as f32) in point order.  Outputs, caller-owned, sized for max_voxels:
+ * voxels [max_voxels, max_points_per_voxel, num_point_features] f32 (zeroed
+ * first when clear_voxels; with empty_mean the empty slots of every voxel get
+ * its mean, utils.py:145-152), indices [max_voxels, ndim] int32 in ZYX order,
+ * num_per_voxel [max_voxels] int32 (clamped counts), pc_voxel_id [n_points]
+ * int64 (voxel of every point, -1 when dropped) and *num_voxels.  Blocks the
+ * host once, to read the voxel count. */
+int sp_point2voxel(const void* points, int32_t dtype, int64_t n_points, int64_t point_cols,
+                   int32_t ndim, const double* vsize_xyz, const double* coors_min_xyz,
+                   const int64_t* grid_size_xyz, int32_t num_point_features, int64_t max_voxels,
+                   int32_t max_points_per_voxel, int32_t clear_voxels, int32_t empty_mean,
+                   float* voxels, int32_t* indices, int32_t* num_per_voxel,
+                   int64_t* pc_voxel_id, int64_t* num_voxels, void* ws, size_t ws_bytes,
+                   void* stream);
+
+/* ---- hash table (spconv_triton/pytorch/hash.py:15-110) ----------------- */
+/* A table of `capacity` (a power of two) slots lives in one caller-owned
+ * device buffer of sp_hash_table_bytes(capacity).  Keys are int32 (key64 = 0)
+ * or int64 (key64 = 1; the key INT64_MAX is reserved); values hold 4 or 8
+ * bytes, vkind 0 int32, 1 int64, 2 f32, 3 f64.  `epoch` must grow with every
+ * insert call on a table: among writers of one key the last call, and in it
+ * the last position, wins (the reference's sort-based insert, hash.py:38-59). */
+size_t sp_hash_table_bytes(int64_t capacity);
+/* Workspace of an insert of n keys (n = 0: of items / assign_arange). */
+size_t sp_hash_workspace_size(int64_t capacity, int64_t n);
+/* Empties the table. */
+int sp_hash_clear(void* table, int64_t capacity, void* stream);
+/* HashTable.insert (hash.py:38-59); values may be NULL (zeros).  Blocks the
+ * host once: *n_entries receives the number of stored keys, and a full table
+ * fails with SP_ERR_HASH_FULL. */
+int sp_hash_insert(void* table, int64_t capacity, const void* keys, int32_t key64,
+                   const void* values, int32_t vkind, int64_t n, uint32_t epoch,
+                   int64_t* n_entries, void* ws, size_t ws_bytes, void* stream);
+/* HashTable.insert_exist_keys (hash.py:79-89): updates stored keys only;
+ * found [n] uint8 receives 1 where the key was stored. */
+int sp_hash_insert_existing(void* table, int64_t capacity, const void* keys, int32_t key64,
+                            const void* values, int32_t vkind, int64_t n, uint32_t epoch,
+                            uint8_t* found, void* ws, size_t ws_bytes, void* stream);
+/* HashTable.query (hash.py:61-77): values_out [n] (0 where absent) and
+ * is_empty [n] uint8. */
+int sp_hash_query(const void* table, int64_t capacity, const void* keys, int32_t key64,
+                  int32_t vkind, int64_t n, void* values_out, uint8_t* is_empty, void* stream);
+/* HashTable.items / assign_arange_ (hash.py:91-110): the stored entries in
+ * ascending key order.  assign_arange = 0: the first min(count, max_items)
+ * keys and values go to keys_out / values_out; assign_arange = 1: the value
+ * of the i-th key becomes i (in the value type).  The count is left in the
+ * table's header word 2 (device memory, byte offset 8). */
+int sp_hash_items(void* table, int64_t capacity, int32_t key64, int32_t vkind, int64_t max_items,
+                  void* keys_out, void* values_out, int32_t assign_arange, void* ws,
+                  size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

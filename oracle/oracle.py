@@ -13,6 +13,8 @@ It restates the reference's host flow in numpy around the C kernels of
 * ``native_pair_to_tables`` follows ``pairs.py:429-469``
 * ``gemm_*`` follow ``_impl/gemm.py:254-321`` (fwd / dgrad) and ``:356-426`` (wgrad)
 * ``maxpool_*`` / ``avgpool_*`` follow ``_impl/pool.py:45-257``
+* ``point_to_voxel`` follows ``spconv_triton/pytorch/utils.py:16-163``
+* ``hash_sparse_add`` follows ``spconv_triton/pytorch/functional.py:417-490``
 
 Every function returns numpy arrays; integer outputs are the exact values the
 reference produces (keys are widened to int64, which the reference proves
@@ -404,6 +406,87 @@ def avgpool_bwd(G, count, pb):
     getattr(lib(), f"orc_avgpool_bwd_{suf}")(_p(Gw), _p(count), ctypes.c_int64(C), _p(pb),
                                              ctypes.c_int64(kv), ctypes.c_int64(n_in), _p(dX))
     return dX.astype(G.dtype)
+
+
+def point_to_voxel(points, vsize_xyz, coors_range_xyz, num_point_features, max_num_voxels,
+                   max_num_points_per_voxel, empty_mean=False):
+    """First-come-first-served voxelisation (reference utils.py:16-163), in
+    numpy.  Quantisation is floor((p - cmin) / vsize) in the points' dtype;
+    voxels are numbered by their first point, capped at max_num_voxels; a
+    voxel stores up to max_num_points_per_voxel points in point order.
+    Returns (voxels [nv, maxpts, F] f32 with zeros in empty slots -- or the
+    voxel's mean with empty_mean --, indices [nv, ndim] int32 ZYX,
+    num_per_voxel [nv] int32, pc_voxel_id [n] int64)."""
+    pts = np.asarray(points)
+    ndim = len(vsize_xyz)
+    n = pts.shape[0]
+    cmin = np.asarray(coors_range_xyz[:ndim], dtype=pts.dtype)
+    vsize = np.asarray(vsize_xyz, dtype=pts.dtype)
+    grid = [round((coors_range_xyz[ndim + i] - coors_range_xyz[i]) / vsize_xyz[i])
+            for i in range(ndim)]
+    with np.errstate(invalid="ignore"):
+        q = np.floor((pts[:, :ndim] - cmin) / vsize)
+        in_range = ((q >= 0) & (q < np.asarray(grid, dtype=pts.dtype))).all(1)
+    pc_voxel_id = np.full(n, -1, dtype=np.int64)
+    maxpts = max_num_points_per_voxel
+    empty = (np.zeros((0, maxpts, num_point_features), np.float32), np.zeros((0, ndim), np.int32),
+             np.zeros(0, np.int32), pc_voxel_id)
+    valid = np.nonzero(in_range)[0]
+    if valid.size == 0:
+        return empty
+    qv = q[valid].astype(np.int64)
+    lin = qv[:, 0].copy()
+    for d in range(1, ndim):
+        lin = lin * grid[d] + qv[:, d]
+    uniq, first, inverse = np.unique(lin, return_index=True, return_inverse=True)
+    order = np.argsort(first, kind="stable")          # voxels by first occurrence
+    vid_of_uniq = np.empty_like(order)
+    vid_of_uniq[order] = np.arange(uniq.size)
+    vid = vid_of_uniq[inverse.reshape(-1)]
+    nv = min(uniq.size, max_num_voxels)
+    kept = vid < nv
+    counts = np.bincount(vid[kept], minlength=nv)
+    npv = np.minimum(counts, maxpts).astype(np.int32)
+    rem = uniq[order][:nv]
+    coords = np.empty((nv, ndim), np.int64)
+    for d in range(ndim - 1, -1, -1):
+        coords[:, d] = rem % grid[d]
+        rem = rem // grid[d]
+    voxels = np.zeros((nv, maxpts, num_point_features), np.float32)
+    slot = np.zeros(nv, np.int64)
+    for i, v in zip(valid[kept], vid[kept]):          # point order: arrival order per voxel
+        if slot[v] < maxpts:
+            voxels[v, slot[v]] = pts[i, :num_point_features].astype(np.float32)
+        slot[v] += 1
+    pc_voxel_id[valid[kept]] = vid[kept]
+    if empty_mean:
+        sums = voxels.sum(axis=1, dtype=np.float32)
+        means = sums / np.maximum(npv, 1)[:, None].astype(np.float32)
+        for v in range(nv):
+            voxels[v, npv[v]:] = means[v]
+    return voxels, coords[:, ::-1].astype(np.int32), npv, pc_voxel_id
+
+
+def hash_sparse_add(indices_list, features_list, shape):
+    """Union of coordinates in ascending batch-major key order, features of
+    equal coordinates summed in input order (reference functional.py:429-490
+    with its sorted-array HashTable, hash.py:38-98)."""
+    keys = []
+    for ind in indices_list:
+        ind = np.asarray(ind, dtype=np.int64)
+        k = ind[:, 0].copy()
+        for d in range(1, ind.shape[1]):
+            k = k * int(shape[d]) + ind[:, d]
+        keys.append(k)
+    uniq = np.unique(np.concatenate(keys))
+    C = np.asarray(features_list[0]).shape[1]
+    feats = np.zeros((uniq.size, C), dtype=np.asarray(features_list[0]).dtype)
+    out_ind = np.zeros((uniq.size, np.asarray(indices_list[0]).shape[1]), np.int32)
+    for k, ind, f in zip(keys, indices_list, features_list):
+        rows = np.searchsorted(uniq, k)
+        feats[rows] += np.asarray(f)
+        out_ind[rows] = ind
+    return out_ind, feats
 
 
 if os.environ.get("SPCONV_ORACLE_THREADS"):

@@ -119,6 +119,19 @@ _SIGNATURES = {
     "sp_maxpool_bwd": (ctypes.c_int, [_P, _P, _P, _I32, _I64, _I64, _P, _I64, _I64, _P, _P]),
     "sp_avgpool_fwd": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _I64, _I64, _P, _P, _P]),
     "sp_avgpool_bwd": (ctypes.c_int, [_P, _P, _I32, _I64, _I64, _P, _I64, _I64, _P, _P]),
+    "sp_point2voxel_workspace_size": (_SZ, [_I64, _I64]),
+    "sp_point2voxel": (ctypes.c_int, [_P, _I32, _I64, _I64, _I32, _P, _P, _P, _I32, _I64, _I32,
+                                      _I32, _I32, _P, _P, _P, _P, ctypes.POINTER(_I64), _P, _SZ,
+                                      _P]),
+    "sp_hash_table_bytes": (_SZ, [_I64]),
+    "sp_hash_workspace_size": (_SZ, [_I64, _I64]),
+    "sp_hash_clear": (ctypes.c_int, [_P, _I64, _P]),
+    "sp_hash_insert": (ctypes.c_int, [_P, _I64, _P, _I32, _P, _I32, _I64, _U32,
+                                      ctypes.POINTER(_I64), _P, _SZ, _P]),
+    "sp_hash_insert_existing": (ctypes.c_int, [_P, _I64, _P, _I32, _P, _I32, _I64, _U32, _P, _P,
+                                               _SZ, _P]),
+    "sp_hash_query": (ctypes.c_int, [_P, _I64, _P, _I32, _I32, _I64, _P, _P, _P]),
+    "sp_hash_items": (ctypes.c_int, [_P, _I64, _I32, _I32, _I64, _P, _P, _I32, _P, _SZ, _P]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

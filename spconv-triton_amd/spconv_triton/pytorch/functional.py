@@ -14,6 +14,7 @@ from torch.autograd.function import once_differentiable
 
 from spconv_triton.compat import tv
 from spconv_triton.pytorch import ops
+from spconv_triton.pytorch.hash import HashTable
 from spconv_triton.tools import CUDAKernelTimer
 
 _FWD = torch.amp.custom_fwd(cast_inputs=torch.float16, device_type="cuda")
@@ -204,3 +205,88 @@ indice_subm_conv = SubMConvFunction.apply
 indice_maxpool = SparseMaxPoolFunction.apply
 indice_maxpool_implicit_gemm = SparseMaxPoolImplicitGemmFunction.apply
 indice_avgpool_implicit_gemm = SparseAvgPoolImplicitGemmFunction.apply
+
+
+_MAX_INT32 = 2 ** 31 - 1
+
+
+def _indice_to_scalar(indices: torch.Tensor, shape: list[int]) -> torch.Tensor:
+    """Batch-major linear key of [b, c0, c1, ...] rows (reference
+    functional.py:417-426)."""
+    if indices.shape[1] != len(shape):
+        raise AssertionError
+    stride = [1] * len(shape)
+    for i in range(len(shape) - 2, -1, -1):
+        stride[i] = stride[i + 1] * shape[i + 1]
+    scalar = indices[:, -1].clone()
+    for i in range(len(shape) - 1):
+        scalar += stride[i] * indices[:, i]
+    return scalar.contiguous()
+
+
+def _check_same_space(tens):
+    first = tens[0]
+    for ten in tens:
+        if ten.spatial_shape != first.spatial_shape:
+            raise AssertionError
+        if ten.batch_size != first.batch_size:
+            raise AssertionError
+        if ten.features.shape[1] != first.features.shape[1]:
+            raise AssertionError
+
+
+def _finish_add(tens, feats, inds):
+    from spconv_triton.pytorch.core import SparseConvTensor
+
+    first = tens[0]
+    res = SparseConvTensor(feats, inds, first.spatial_shape, first.batch_size,
+                           benchmark=first.benchmark)
+    largest = max(range(len(tens)), key=lambda i: (tens[i].features.shape[0], -i))
+    if feats.shape[0] == tens[largest].features.shape[0]:
+        res.indice_dict = tens[largest].indice_dict
+    res.benchmark_record = first.benchmark_record
+    res._timer = first._timer
+    res.thrust_allocator = first.thrust_allocator
+    return res
+
+
+def sparse_add_hash_based(*tens):
+    """Sum of sparse tensors with different coordinate sets (reference
+    functional.py:429-490): every coordinate's linear key goes into a device
+    HashTable, the stored keys are numbered in ascending order
+    (assign_arange_), and each input's features are added into the rows of
+    its keys, in input order."""
+    _check_same_space(tens)
+    first = tens[0]
+    shape = [first.batch_size, *first.spatial_shape]
+    whole = 1
+    for v in shape:
+        whole *= int(v)
+    key64 = whole >= _MAX_INT32
+    table = HashTable(first.features.device, torch.int64 if key64 else torch.int32, torch.int32,
+                      2 * sum(t.features.shape[0] for t in tens))
+    scalars = []
+    for ten in tens:
+        ind = ten.indices.long() if key64 else ten.indices
+        scalar = _indice_to_scalar(ind, shape)
+        scalars.append(scalar)
+        table.insert(scalar)
+    count = int(table.assign_arange_().item())
+    feat = first.features
+    out_features = torch.zeros([count, feat.shape[1]], dtype=feat.dtype, device=feat.device)
+    out_indices = torch.zeros([count, first.indices.shape[1]], dtype=first.indices.dtype,
+                              device=first.indices.device)
+    for ten, scalar in zip(tens, scalars):
+        rows, _ = table.query(scalar)
+        rows = rows.long()
+        out_features[rows] += ten.features
+        out_indices[rows] = ten.indices
+    return _finish_add(tens, out_features, out_indices)
+
+
+def sparse_add(*tens):
+    """Sum of sparse tensors (reference functional.py:493-535, a coalesced
+    torch.sparse sum): the union of the coordinates in ascending batch-major
+    order with the features of equal coordinates added in input order -- the
+    same result as sparse_add_hash_based."""
+    return sparse_add_hash_based(*tens)

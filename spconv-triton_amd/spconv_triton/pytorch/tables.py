@@ -47,6 +47,16 @@ class AddTable(SparseModule):
         return out_size
 
 
+class AddTableMisaligned(SparseModule):
+    """Adds sparse tensors of one shape with different coordinates (reference
+    tables.py:78-82)."""
+
+    def forward(self, inputs: list[SparseConvTensor]):
+        from spconv_triton.pytorch import functional as F
+
+        return F.sparse_add_hash_based(*inputs)
+
+
 class ConcatTable(SparseModule):
     def forward(self, x):
         return [module(x) for module in self._modules.values()]

@@ -118,9 +118,14 @@ def test_public_api_matches_reference():
     for name in api["top"]:
         assert hasattr(spconv_triton, name), name
     for name in api["functional"]:
-        if name.startswith("sparse_add"):
-            continue  # sparse_add is outside the hot path
         assert hasattr(spconv.functional, name), name
+    from spconv_triton.pytorch import hash as sp_hash
+    from spconv_triton.pytorch import utils as sp_utils
+
+    for name in api["hash"]:
+        assert hasattr(sp_hash, name), name
+    for name in api["pytorch_utils"]:
+        assert hasattr(sp_utils, name), name
     for cls, args in api["ctors"].items():
         params = list(inspect.signature(getattr(spconv, cls).__init__).parameters)[1:]
         assert params == args, f"{cls}: {params} != {args}"

@@ -287,3 +287,68 @@ def test_oracle_gemm_against_dense_conv():
     dW = orc.gemm_wgrad(X, G, res[2], K, C)
     assert abs(lhs - float((dX * X).sum())) < 1e-9 * max(1.0, abs(lhs))
     assert abs(lhs - float((dW * W.reshape(K, 27, C)).sum())) < 1e-9 * max(1.0, abs(lhs))
+
+
+def _canon_voxels(idx, vox, npv):
+    """Voxels sorted by coordinate, points inside a voxel sorted
+    lexicographically (the reference's canonical form, tests/helpers.py:442-465)."""
+    idx = np.asarray(idx, np.int64)
+    vox = np.asarray(vox, np.float64)
+    npv = np.asarray(npv, np.int64)
+    if idx.shape[0] == 0:
+        return idx, vox, npv
+    maxc = int(idx.max()) + 2
+    key = np.zeros(idx.shape[0], np.int64)
+    for d in range(idx.shape[1]):
+        key = key * maxc + idx[:, d]
+    order = np.argsort(key, kind="stable")
+    idx, vox, npv = idx[order], vox[order].copy(), npv[order]
+    for i in range(vox.shape[0]):
+        n = int(min(npv[i], vox.shape[1]))
+        pts = vox[i, :n]
+        pkey = pts[:, 0].copy()
+        for d in range(1, pts.shape[1]):
+            pkey = pkey * 131071.0 + pts[:, d]
+        vox[i, :n] = pts[np.argsort(pkey, kind="stable")]
+    return idx, vox, npv
+
+
+@pytest.mark.parametrize("case_id", ["p2v_cpu_basic", "p2v_cpu_trunc", "p2v_cpu_cap",
+                                     "p2v1d_basic", "p2v4d_basic"])
+def test_oracle_point_to_voxel_golden(golden, case_id):
+    """The oracle's voxelisation against spconv 2.3.8's (the reference's
+    goldens): bitwise for the first-come-first-served CPU cases, in the
+    reference's canonical form for the others."""
+    case = golden("ext_p2v.pt", case_id)
+    ctor = case["ctor"]
+    vox, idx, npv, pcvid = orc.point_to_voxel(
+        case["points"].numpy(), ctor["vsize_xyz"], ctor["coors_range_xyz"],
+        ctor["num_point_features"], ctor["max_num_voxels"], ctor["max_num_points_per_voxel"])
+    expect = case["expect"]
+    if case["kind"] == "p2v_cpu":
+        np.testing.assert_array_equal(idx, expect["indices"].numpy())
+        np.testing.assert_array_equal(npv, expect["num_per_voxel"].numpy())
+        np.testing.assert_array_equal(pcvid, expect["pc_voxel_id"].numpy())
+        np.testing.assert_array_equal(vox, expect["voxels"].numpy())
+    else:
+        ic, vc, nc = _canon_voxels(idx, vox, npv)
+        np.testing.assert_array_equal(ic, expect["indices_canon"].numpy())
+        np.testing.assert_array_equal(nc, expect["num_per_voxel_canon"].numpy())
+        if expect["check_contents"]:
+            np.testing.assert_allclose(vc, expect["voxels_canon"].numpy(), atol=1e-5, rtol=0)
+
+
+@pytest.mark.parametrize("case_id", ["sparse_add", "sparse_add_hash_based",
+                                     "add_table_misaligned"])
+def test_oracle_sparse_add_golden(golden, case_id):
+    case = golden("misc.pt", case_id)
+    a, b = case["inputs"]
+    shape = [a["batch_size"], *a["spatial_shape"]]
+    ind, feats = orc.hash_sparse_add([a["indices"].numpy(), b["indices"].numpy()],
+                                     [a["features"].numpy(), b["features"].numpy()], shape)
+    expect = case["expect"]
+    order = canonical_order(ind, a["spatial_shape"])
+    np.testing.assert_array_equal(order, np.arange(ind.shape[0]))  # already ascending
+    np.testing.assert_array_equal(ind, expect["out_indices"].numpy())
+    np.testing.assert_allclose(feats, expect["out_features"].numpy(), atol=expect["atol_out"],
+                               rtol=0)
