@@ -552,6 +552,7 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
         rrec, i < n_items ? uint32_t(i) * 512u + rec_lane : kOob, 0, 0);
   };
 
+  const uint32_t zaddr = chunk_base(uint32_t(U));  // the tile's zero row
   for (int rc = 0; rc < nrc; ++rc) {
     const uint32_t bofs = uint32_t(rc * 4 + gp) * slab_bytes + bpiece;
     auto gload = [&](uint32_t kb) -> uint4 {  // this thread's piece of an item's B slab
@@ -596,6 +597,18 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
     frag fa[2][2][2], fb[2][2][2];  // [item parity][ks][mt or nt]
     uint4 q[4];                     // B pieces loaded, not yet in the ring: item i in q[i % 4]
     uint32_t r[4];                  // A address records: item i in r[i % 4]
+    // A 32-row block of an item whose rows all read the zero row (no pair in
+    // the block, or a padding item) multiplies zeros.  With fp32 operands
+    // (4 MFMAs of 64 clocks per fragment pair, the MFMA pipe is the limit)
+    // its MFMAs are skipped; the test is a wave ballot, so the branch is
+    // uniform.  For 16-bit operands the MFMAs are not the limit and the test
+    // costs more than it saves (measured at the metric shape), so it is
+    // compiled out.
+    constexpr bool kSkipDead = sizeof(T) == 4;
+    bool live[2][2] = {{true, true}, {true, true}};  // [item parity][mt]
+    auto block_live = [&](uint32_t addr) -> bool {
+      return !kSkipDead || __builtin_amdgcn_ballot_w64(addr != zaddr) != 0;
+    };
     {
       const uint4 p0 = gload(s_kb[0]), p1 = gload(s_kb[1]), p2 = gload(s_kb[2]);
       r[0] = load_rec(0);
@@ -611,6 +624,10 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
       lds_barrier();
       read_b(0, fb[0]);
       read_a(r[0], fa[0]);
+      if constexpr (kSkipDead) {
+        live[0][0] = block_live(r[0] & 0xffffu);
+        live[0][1] = block_live(r[0] >> 16);
+      }
       r[0] = load_rec(4);
       lds_barrier();  // the prologue counts as an odd step (slot 0 is rewritten in step 1)
     }
@@ -637,9 +654,13 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
                                                    uint32_t(nt * 32 + l32) * 16u);
       };
       auto mma = [&](int ks, int mt, int nt) {
-        Mfma<T>::mma(ac[ks][mt], bc[ks][nt], acc[mt][nt]);
+        if (!kSkipDead || live[j % 2][mt]) Mfma<T>::mma(ac[ks][mt], bc[ks][nt], acc[mt][nt]);
         __builtin_amdgcn_sched_barrier(0);
       };
+      if constexpr (kSkipDead) {
+        live[(j + 1) % 2][0] = block_live(t2[0]);
+        live[(j + 1) % 2][1] = block_live(t2[1]);
+      }
       // first LDS operation of the step: the B load below waits for it, and
       // LDS operations complete in order, so issued last it would make that
       // wait drain every fragment read of the step
