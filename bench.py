@@ -184,7 +184,7 @@ def main() -> int:
         s.record()
         res = pairgen()
         m.record()
-        gemm_impl.gather_plan(res[2], N_VOXELS)  # synchronizes once (overflow count)
+        gemm_impl.gather_plan(res[2], N_VOXELS)
         e.record()
         torch.cuda.synchronize()
         pg.append(s.elapsed_time(e))
@@ -253,7 +253,8 @@ def main() -> int:
     tfile = ROOT / "profiles" / "gather_gemm_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
-    plan, n_overflow = gemm_impl.gather_plan(y0.indice_dict["subm0"].pair_fwd, N_VOXELS)
+    plan = gemm_impl.gather_plan(y0.indice_dict["subm0"].pair_fwd, N_VOXELS)
+    n_overflow = gemm_impl.plan_overflow_count(plan)
     nbytes = gemm_bytes(N_VOXELS, N_VOXELS, plan_read_bytes(plan, KV, N_VOXELS))
     flops = 2.0 * n_pairs * C_IN * C_OUT
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9

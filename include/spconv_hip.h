@@ -181,21 +181,22 @@ int sp_conv_gemm_packed(const void* a, int32_t dtype, int64_t n_src, const void*
  * (spconv_triton/pytorch/_impl/pairs.py:429-469 native_pair_to_tables,
  * gemm.py:661-669 valid_signal).  No reference entry point corresponds to it.
  * sp_gather_plan_bytes returns 0 when kv is outside 1..64 (no plan: use
- * sp_conv_gemm_packed).  sp_gather_plan_build synchronizes the stream once and
- * returns in *n_overflow the number of tiles whose distinct rows do not fit in
- * LDS (they are gathered directly from memory). */
+ * sp_conv_gemm_packed).  sp_gather_plan_build is asynchronous; n_overflow
+ * (nullable) requests the number of tiles whose distinct rows do not fit in
+ * LDS (the GEMM gathers those directly from memory), which costs one stream
+ * synchronization. */
 size_t sp_gather_plan_bytes(int64_t M, int64_t kv);
 int sp_gather_plan_build(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_src, void* plan,
                          size_t plan_bytes, int64_t* n_overflow, void* stream);
 
 /* sp_conv_gemm_packed with a gather plan of `pairs` (built for the same kv, M
- * and n_src) and the n_overflow its build returned; no mask tables.  Results
- * are bit-identical to sp_conv_gemm_packed's.  Replaces the same reference
- * kernels as sp_conv_fwd / sp_conv_dgrad (gemm.py:206-321). */
+ * and n_src); no mask tables.  One kernel launch.  Results are bit-identical
+ * to sp_conv_gemm_packed's.  Replaces the same reference kernels as
+ * sp_conv_fwd / sp_conv_dgrad (gemm.py:206-321). */
 int sp_conv_gemm_planned(const void* a, int32_t dtype, int64_t n_src, const void* packed,
                          int64_t K, int64_t kv, int64_t C, int32_t transpose, int32_t has_bias,
                          const int32_t* pairs, int64_t M, const void* plan, size_t plan_bytes,
-                         int64_t n_overflow, void* out, int32_t out_dtype, void* stream);
+                         void* out, int32_t out_dtype, void* stream);
 
 /* Forward: out[m, n] = bias[n] + sum_k sum_c X[pf[k, m], c] * W[n, k, c].
  * X [n_in, C] dtype; W [K, kv, C] w_dtype; pf [kv, n_out]; bias [K] of

@@ -262,31 +262,25 @@ __host__ __device__ inline DirectLds direct_lds(int E, uint32_t out_size) {
   return l;
 }
 
-// All tiles (plan.count == nullptr) or, with a plan, the overflow tiles only,
-// one workgroup per list entry.
+// One (tile, 64-column block) of the direct kernel, the whole workgroup:
+// every tile of an unplanned call, and the tiles of a planned call whose
+// distinct rows do not fit in LDS.  Uses direct_lds(min(kv, 64) + kPad) bytes
+// of `smem`.
 template <typename T, typename OutT, bool VEC>
-__global__ __launch_bounds__(256, 2) void gather_gemm_direct(
-    const T* __restrict__ A, const T* __restrict__ Bt, const int32_t* __restrict__ pairs,
-    PlanDev plan, const float* __restrict__ bias, OutT* __restrict__ out, GemmBufs nb,
-    int64_t n_src, int64_t M, int N, int R, int Rp, int kv) {
+__device__ __forceinline__ void direct_tile(const T* __restrict__ A, const T* __restrict__ Bt,
+                                            const int32_t* __restrict__ pairs,
+                                            const float* __restrict__ bias,
+                                            OutT* __restrict__ out, const GemmBufs& nb,
+                                            int64_t n_src, int64_t M, int N, int R, int Rp,
+                                            int kv, int64_t tile, int n0, unsigned char* smem) {
   using frag = typename Mfma<T>::frag;
   constexpr int V = Mfma<T>::V;
   constexpr uint32_t ES = sizeof(T);
   constexpr int kChunk = kChunkBytes / int(ES);  // reduction elements per item
-  extern __shared__ __align__(16) unsigned char smem[];
 
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int h = lane >> 5, l32 = lane & 31;
-  int64_t tile;
-  if (plan.count != nullptr) {
-    if (int(blockIdx.x) >= *plan.n_overflow) return;
-    tile = plan.overflow[blockIdx.x];
-    if (tile < 0 || tile * kTileRows >= M) return;
-  } else {
-    tile = xcd_tile(blockIdx.x, gridDim.x);
-  }
   const int64_t slot0 = tile * kTileRows + wave * 64;
-  const int n0 = blockIdx.y * 64;
   const int64_t my_row = slot0 + lane;
   const bool row_ok = my_row < M;
 
@@ -419,6 +413,17 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_direct(
                    slot0, n0, M, N, lane);
 }
 
+// Every tile of an unplanned call, one workgroup per (tile, 64 columns).
+template <typename T, typename OutT, bool VEC>
+__global__ __launch_bounds__(256, 2) void gather_gemm_direct(
+    const T* __restrict__ A, const T* __restrict__ Bt, const int32_t* __restrict__ pairs,
+    const float* __restrict__ bias, OutT* __restrict__ out, GemmBufs nb, int64_t n_src,
+    int64_t M, int N, int R, int Rp, int kv) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  direct_tile<T, OutT, VEC>(A, Bt, pairs, bias, out, nb, n_src, M, N, R, Rp, kv,
+                            xcd_tile(blockIdx.x, gridDim.x), int(blockIdx.y) * 64, smem);
+}
+
 // ---------------------------------------------------------------------------
 // staged kernel
 // ---------------------------------------------------------------------------
@@ -444,12 +449,13 @@ __host__ __device__ inline StagedLds staged_lds(int E, uint32_t out_size) {
   return l;
 }
 
-// Tiles of the plan that fit in LDS (plan required, kv <= kPlanMaxKv).
+// Every tile of a planned call (kv <= kPlanMaxKv): staged when its distinct
+// rows fit in LDS, else (an overflow tile) by the direct path.
 template <typename T, typename OutT, bool VEC>
 __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
-    const T* __restrict__ A, const T* __restrict__ Bt, PlanDev plan,
-    const float* __restrict__ bias, OutT* __restrict__ out, GemmBufs nb, int64_t M, int N,
-    int R, int Rp, int kv) {
+    const T* __restrict__ A, const T* __restrict__ Bt, const int32_t* __restrict__ pairs,
+    PlanDev plan, const float* __restrict__ bias, OutT* __restrict__ out, GemmBufs nb,
+    int64_t n_src, int64_t M, int N, int R, int Rp, int kv) {
   using frag = typename Mfma<T>::frag;
   constexpr int V = Mfma<T>::V;
   constexpr uint32_t ES = sizeof(T);
@@ -495,7 +501,10 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
   }
   const int nact = plan.nact[tile];
   const int32_t ko = tid < E ? plan.koff[tile * E + tid] : -1;
-  if (U >= kLdsRows) return;  // whole workgroup: an overflow tile
+  if (U >= kLdsRows) {  // whole workgroup: an overflow tile
+    direct_tile<T, OutT, VEC>(A, Bt, pairs, bias, out, nb, n_src, M, N, R, Rp, kv, tile, n0, smem);
+    return;
+  }
   // byte offsets of the rows in A, kept in LDS (not registers) while the
   // K-loop runs; the four threads of a row write the same value
   uint32_t* s_rowoff = reinterpret_cast<uint32_t*>(smem + L.rowoff_off);

@@ -295,7 +295,6 @@ struct GemmCall {
   int N, R, Rp, kv;
   bool planned;
   PlanDev plan;
-  int64_t n_overflow;  // overflow tiles of the plan (run by the direct kernel)
   const float* bias;
   bool vec;
 };
@@ -311,7 +310,7 @@ static int allow_lds(const void* kern, uint32_t bytes, bool& done) {
 
 template <typename T, typename OutT, bool VEC>
 static int launch_direct(dim3 grid, hipStream_t s, const T* A, const T* bt, const int32_t* pairs,
-                         OutT* o, GemmBufs nb, const GemmCall& c, PlanDev plan) {
+                         OutT* o, GemmBufs nb, const GemmCall& c) {
   const int G = c.kv < kGroupOffsets ? c.kv : kGroupOffsets;
   const uint32_t lds = direct_lds(G + kPad, uint32_t(sizeof(OutT))).total;
   auto kern = gather_gemm_direct<T, OutT, VEC>;
@@ -319,39 +318,42 @@ static int launch_direct(dim3 grid, hipStream_t s, const T* A, const T* bt, cons
   int rc = allow_lds(reinterpret_cast<const void*>(kern),
                      direct_lds(kGroupOffsets + kPad, uint32_t(sizeof(OutT))).total, attr_set);
   if (rc) return rc;
-  kern<<<grid, 256, lds, s>>>(A, bt, pairs, plan, c.bias, o, nb, c.n_src, c.M, c.N, c.R, c.Rp,
+  kern<<<grid, 256, lds, s>>>(A, bt, pairs, c.bias, o, nb, c.n_src, c.M, c.N, c.R, c.Rp, c.kv);
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+// LDS of the staged kernel: its own layout, or the direct path's for an
+// overflow tile (smaller for every kv the plans cover; the max keeps it safe).
+static uint32_t staged_kernel_lds(int E, int kv, uint32_t out_size) {
+  const uint32_t a = staged_lds(E, out_size).total;
+  const int G = kv < kGroupOffsets ? kv : kGroupOffsets;
+  const uint32_t b = direct_lds(G + kPad, out_size).total;
+  return a > b ? a : b;
+}
+
+template <typename T, typename OutT, bool VEC>
+static int launch_staged(dim3 grid, hipStream_t s, const T* A, const T* bt, const int32_t* pairs,
+                         OutT* o, GemmBufs nb, const GemmCall& c) {
+  const uint32_t lds = staged_kernel_lds(c.plan.E, c.kv, uint32_t(sizeof(OutT)));
+  auto kern = gather_gemm_staged<T, OutT, VEC>;
+  static bool attr_set = false;
+  int rc = allow_lds(reinterpret_cast<const void*>(kern),
+                     staged_kernel_lds(kPlanMaxKv, kPlanMaxKv, uint32_t(sizeof(OutT))), attr_set);
+  if (rc) return rc;
+  kern<<<grid, 256, lds, s>>>(A, bt, pairs, c.plan, c.bias, o, nb, c.n_src, c.M, c.N, c.R, c.Rp,
                               c.kv);
   SP_LAUNCHED();
   return SP_OK;
 }
 
-template <typename T, typename OutT, bool VEC>
-static int launch_staged(dim3 grid, hipStream_t s, const T* A, const T* bt, OutT* o, GemmBufs nb,
-                         const GemmCall& c) {
-  const uint32_t lds = staged_lds(c.plan.E, uint32_t(sizeof(OutT))).total;
-  auto kern = gather_gemm_staged<T, OutT, VEC>;
-  static bool attr_set = false;
-  int rc = allow_lds(reinterpret_cast<const void*>(kern),
-                     staged_lds(kPlanMaxKv, uint32_t(sizeof(OutT))).total, attr_set);
-  if (rc) return rc;
-  kern<<<grid, 256, lds, s>>>(A, bt, c.plan, c.bias, o, nb, c.M, c.N, c.R, c.Rp, c.kv);
-  SP_LAUNCHED();
-  return SP_OK;
-}
-
-// Planned call: the staged kernel over all tiles (it skips overflow tiles),
-// then the direct kernel over the overflow list when there is one.
-// Unplanned call: the direct kernel over all tiles.
+// Planned call: the staged kernel over all tiles (overflow tiles take its
+// direct path).  Unplanned call: the direct kernel over all tiles.
 template <typename T, typename OutT, bool VEC>
 static int launch_modes(unsigned gx, unsigned gy, hipStream_t s, const T* A, const T* bt,
                         const int32_t* pairs, OutT* o, GemmBufs nb, const GemmCall& c) {
-  const PlanDev none{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0};
-  if (!c.planned)
-    return launch_direct<T, OutT, VEC>(dim3{gx, gy, 1u}, s, A, bt, pairs, o, nb, c, none);
-  int rc = launch_staged<T, OutT, VEC>(dim3{gx, gy, 1u}, s, A, bt, o, nb, c);
-  if (rc || c.n_overflow == 0) return rc;
-  return launch_direct<T, OutT, VEC>(dim3{unsigned(c.n_overflow), gy, 1u}, s, A, bt, pairs, o, nb,
-                                     c, c.plan);
+  if (!c.planned) return launch_direct<T, OutT, VEC>(dim3{gx, gy, 1u}, s, A, bt, pairs, o, nb, c);
+  return launch_staged<T, OutT, VEC>(dim3{gx, gy, 1u}, s, A, bt, pairs, o, nb, c);
 }
 
 // The mask tables (pair_mask / mask_argsort) of the reference's masked path
@@ -398,13 +400,11 @@ static int launch_gemm_out(int out_dtype, const T* A, const T* bt, const int32_t
   }
 }
 
-// plan (nullable) is a gather plan of `pairs` built by sp_gather_plan_build,
-// which reported n_overflow.
+// plan (nullable) is a gather plan of `pairs` built by sp_gather_plan_build.
 static int gemm_packed(const void* A, int dtype, int64_t n_src, const void* packed, int64_t K,
                        int64_t kv, int64_t C, int transpose, int has_bias, const int32_t* pairs,
                        int64_t M, const int32_t* pm, const int32_t* ar, const void* plan,
-                       size_t plan_bytes, int64_t n_overflow, void* out, int out_dtype,
-                       hipStream_t s) {
+                       size_t plan_bytes, void* out, int out_dtype, hipStream_t s) {
   SP_CHECK_ARG(gemm_dtype_ok(dtype), "gemm: feature dtype %d not supported (f16/bf16/f32)", dtype);
   SP_CHECK_ARG(K >= 1 && C >= 1 && kv >= 1 && M >= 0 && n_src >= 0, "gemm: bad sizes");
   SP_CHECK_ARG(K < 65536 && C < 65536 && kv < 65536, "gemm: channel/kernel size too large");
@@ -425,17 +425,12 @@ static int gemm_packed(const void* A, int dtype, int64_t n_src, const void* pack
   c.vec = (p.R % vec_of(dtype) == 0) && (reinterpret_cast<uintptr_t>(A) % 16 == 0);
   c.planned = plan != nullptr;
   c.plan = PlanDev{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0};
-  c.n_overflow = 0;
   if (plan) {
     SP_CHECK_ARG(kv <= kPlanMaxKv, "gemm: gather plans need kv <= %d", kPlanMaxKv);
     const PlanLayout pl = plan_layout(M, kv);
     SP_CHECK_ARG(plan_bytes >= pl.total, "gemm: plan buffer %zu < %zu bytes", plan_bytes,
                  pl.total);
-    SP_CHECK_ARG(n_overflow >= 0 && n_overflow <= pl.ntiles,
-                 "gemm: n_overflow %lld outside 0..%lld", (long long)n_overflow,
-                 (long long)pl.ntiles);
     c.plan = plan_view(plan, M, kv);
-    c.n_overflow = n_overflow;
   }
   switch (dtype) {
     case SP_F16:
@@ -464,7 +459,7 @@ static int gemm_common(const void* A, int dtype, int64_t n_src, const void* w, i
   int rc = pack_weight(w, w_dtype, bias, K, kv, C, dtype, transpose, ws, s);
   if (rc) return rc;
   return gemm_packed(A, dtype, n_src, ws, K, kv, C, transpose, bias != nullptr, pairs, M, pm, ar,
-                     nullptr, 0, 0, out, out_dtype, s);
+                     nullptr, 0, out, out_dtype, s);
 }
 
 static int wgrad_splits(int64_t kv, int64_t C, int64_t K, int64_t n_rows) {
@@ -504,16 +499,16 @@ int sp_conv_gemm_packed(const void* a, int32_t dtype, int64_t n_src, const void*
                         const int32_t* pairs, int64_t M, const int32_t* pair_mask,
                         const int32_t* mask_argsort, void* out, int32_t out_dtype, void* stream) {
   return gemm_packed(a, dtype, n_src, packed, K, kv, C, transpose, has_bias, pairs, M, pair_mask,
-                     mask_argsort, nullptr, 0, 0, out, out_dtype, as_stream(stream));
+                     mask_argsort, nullptr, 0, out, out_dtype, as_stream(stream));
 }
 
 int sp_conv_gemm_planned(const void* a, int32_t dtype, int64_t n_src, const void* packed,
                          int64_t K, int64_t kv, int64_t C, int32_t transpose, int32_t has_bias,
                          const int32_t* pairs, int64_t M, const void* plan, size_t plan_bytes,
-                         int64_t n_overflow, void* out, int32_t out_dtype, void* stream) {
+                         void* out, int32_t out_dtype, void* stream) {
   SP_CHECK_ARG(plan != nullptr, "gemm: null gather plan");
   return gemm_packed(a, dtype, n_src, packed, K, kv, C, transpose, has_bias, pairs, M, nullptr,
-                     nullptr, plan, plan_bytes, n_overflow, out, out_dtype, as_stream(stream));
+                     nullptr, plan, plan_bytes, out, out_dtype, as_stream(stream));
 }
 
 int sp_conv_fwd(const void* x, int32_t dtype, int64_t n_in, int64_t C, const void* w,

@@ -277,8 +277,7 @@ int sp_gather_plan_build(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_
                kPlanMaxKv);
   SP_CHECK_ARG(M >= 0 && M < (int64_t(1) << 31) && n_src >= 0 && n_src < (int64_t(1) << 31),
                "gather plan: bad sizes M=%lld n_src=%lld", (long long)M, (long long)n_src);
-  SP_CHECK_ARG(n_overflow != nullptr, "gather plan: null n_overflow");
-  *n_overflow = 0;
+  if (n_overflow) *n_overflow = 0;
   if (M == 0) return SP_OK;
   SP_CHECK_ARG(pairs && plan, "gather plan: null pointer");
   const PlanLayout p = plan_layout(M, kv);
@@ -301,10 +300,12 @@ int sp_gather_plan_build(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_
   SP_LAUNCHED();
   plan_overflow_kernel<<<1, 256, 0, s>>>(count, p.ntiles, n_ovf, ovf);
   SP_LAUNCHED();
-  int32_t h = 0;
-  SP_HIP(hipMemcpyAsync(&h, n_ovf, sizeof(h), hipMemcpyDeviceToHost, s));
-  SP_HIP(hipStreamSynchronize(s));
-  *n_overflow = h;
+  if (n_overflow) {  // the count is only reported on request (it costs a sync)
+    int32_t h = 0;
+    SP_HIP(hipMemcpyAsync(&h, n_ovf, sizeof(h), hipMemcpyDeviceToHost, s));
+    SP_HIP(hipStreamSynchronize(s));
+    *n_overflow = h;
+  }
   return SP_OK;
 }
 

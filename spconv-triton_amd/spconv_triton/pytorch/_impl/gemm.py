@@ -96,11 +96,11 @@ USE_GATHER_PLAN = True
 
 
 def gather_plan(pairs: torch.Tensor, n_src: int):
-    """Gather plan of a [kv, M] pair table (``sp_gather_plan_build``) as
-    (plan buffer, number of overflow tiles), or None when kv is outside the
-    planned kernel's range.  Memoised on the table tensor, like the reference
-    memoises its tables on the indice data (pairs.py:429-469); rebuilt if the
-    table is modified in place.  Building synchronizes the stream once."""
+    """Gather plan of a [kv, M] pair table (``sp_gather_plan_build``), or None
+    when kv is outside the planned kernel's range.  Memoised on the table
+    tensor, like the reference memoises its tables on the indice data
+    (pairs.py:429-469); rebuilt if the table is modified in place.  The build
+    is asynchronous (no host synchronization)."""
     kv, M = pairs.shape
     cached = getattr(pairs, "_spconv_triton_plan", None)
     stamp = (int(n_src), pairs._version, pairs.data_ptr())
@@ -111,13 +111,17 @@ def gather_plan(pairs: torch.Tensor, n_src: int):
     if nbytes == 0:
         return None
     plan = torch.empty(nbytes, dtype=torch.uint8, device=pairs.device)
-    n_over = ctypes.c_int64(0)
     _lib.check(L.sp_gather_plan_build(_lib.ptr(pairs), kv, M, int(n_src), _lib.ptr(plan), nbytes,
-                                      ctypes.byref(n_over), _lib.stream_of(pairs.device)),
+                                      None, _lib.stream_of(pairs.device)),
                "sp_gather_plan_build")
-    res = (plan, int(n_over.value))
-    pairs._spconv_triton_plan = (stamp, res)
-    return res
+    pairs._spconv_triton_plan = (stamp, plan)
+    return plan
+
+
+def plan_overflow_count(plan: torch.Tensor) -> int:
+    """Number of tiles of a plan whose distinct rows do not fit in LDS (the
+    plan's first int32; reading it synchronizes)."""
+    return int(plan[:4].view(torch.int32)[0].item())
 
 
 def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: torch.Tensor,
@@ -126,14 +130,13 @@ def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: 
     kv = pairs.shape[0]
     packed = packed_weight(filters, bias, a.dtype, transpose)
     L = _lib.lib()
-    planned = gather_plan(pairs, a.shape[0]) if USE_GATHER_PLAN else None
-    if planned is not None:
+    plan = gather_plan(pairs, a.shape[0]) if USE_GATHER_PLAN else None
+    if plan is not None:
         # the planned kernel skips empty offsets itself: mask tables are not needed
-        plan, n_over = planned
         _lib.check(L.sp_conv_gemm_planned(
             _lib.ptr(a), _lib.dtype_code(a.dtype), a.shape[0], _lib.ptr(packed), K, kv, C,
             int(transpose), int(bias is not None), _lib.ptr(pairs), M, _lib.ptr(plan),
-            plan.numel(), n_over, _lib.ptr(out), _lib.dtype_code(out.dtype),
+            plan.numel(), _lib.ptr(out), _lib.dtype_code(out.dtype),
             _lib.stream_of(a.device)), "sp_conv_gemm_planned")
         return
     _lib.check(L.sp_conv_gemm_packed(

@@ -68,9 +68,9 @@ def _check_plan(pf, n_src):
     from spconv_triton.pytorch._impl import gemm
 
     kv, M = pf.shape
-    res = gemm.gather_plan(pf, n_src)
-    assert res is not None
-    plan, n_over_host = res
+    plan = gemm.gather_plan(pf, n_src)
+    assert plan is not None
+    n_over_host = gemm.plan_overflow_count(plan)
     P = _parse(plan, kv, M)
     p = pf.cpu().numpy()
     overflow = []
@@ -193,8 +193,9 @@ def test_planned_equals_unplanned(ci, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
 def test_planned_overflow_tiles(dtype):
-    """Tiles with too many distinct rows for LDS are left to the direct kernel;
-    mixed with staged tiles the result must not change."""
+    """Tiles with too many distinct rows for LDS take the staged kernel's
+    direct path (same launch); mixed with staged tiles the result must not
+    change."""
     rng = np.random.default_rng(11)
     kv, M, n_src, C, K = 27, 1500, 50_000, 32, 64
     t = rng.integers(0, n_src, size=(kv, M)).astype(np.int32)
