@@ -216,6 +216,89 @@ __global__ __launch_bounds__(256) void subm_probe(const int32_t* __restrict__ id
   }
 }
 
+// ---- subm on a dense grid ---------------------------------------------------
+// When the key volume is small next to the number of rows, a dense cell -> row
+// array replaces the hash: filling it is cheaper than hashing, every probe is
+// one load, and the neighbours of consecutive rows share cache lines.  The
+// probe issues its loads in batches with no dependence between them (the
+// hash's probe chains serialise each thread's kv lookups).  Same results as
+// the hash: an empty cell holds kNoRow, and a cell held by several rows keeps
+// the smallest (atomicMin, like Table32/Table64::insert).
+constexpr int64_t kDenseMaxCells = int64_t(1) << 26;  // 256 MiB of int32
+constexpr int64_t kDenseCellsPerRow = 256;            // beyond this the fill costs more
+constexpr int32_t kNoRow = 0x7fffffff;
+constexpr int kDenseBatch = 9;                        // probe loads in flight per thread
+
+static bool subm_dense(const GeomDev& g, int64_t n) {
+  const double vol = double(g.batch) * double(prod_shape(g.in_shape, g.ndim));
+  return vol <= double(kDenseMaxCells) && vol <= double(kDenseCellsPerRow) * double(n);
+}
+
+static int64_t subm_cells(const GeomDev& g) { return g.batch * prod_shape(g.in_shape, g.ndim); }
+
+// 16-byte stores: the grid is the only large fill of a dense build.
+__global__ __launch_bounds__(256) void fill_i32x4(int32_t* __restrict__ p, int64_t n, int32_t v) {
+  const int64_t n4 = n / 4;
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  int4* q = reinterpret_cast<int4*>(p);
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n4; i += stride)
+    q[i] = make_int4(v, v, v, v);
+  const int64_t t = n4 * 4 + int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t < n) p[t] = v;
+}
+
+__global__ __launch_bounds__(256) void subm_insert_dense(const int32_t* __restrict__ idx,
+                                                         int64_t n, GeomDev g,
+                                                         int32_t* __restrict__ grid) {
+  const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  Coord c = load_coord(idx, r, g);
+  if (!c.ok) return;
+  int64_t acc = c.b;
+  for (int d = 0; d < g.ndim; ++d) acc = acc * g.in_shape[d] + c.x[d];
+  atomicMin(&grid[acc], int32_t(r));
+}
+
+// subm_probe with the dense grid: the same outputs.
+__global__ __launch_bounds__(256) void subm_probe_dense(const int32_t* __restrict__ idx,
+                                                        int64_t n, GeomDev g,
+                                                        const int32_t* __restrict__ grid,
+                                                        int32_t* __restrict__ pf,
+                                                        int32_t* __restrict__ pb,
+                                                        uint32_t* __restrict__ words, int mic) {
+  const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const Coord c = load_coord(idx, r, g);
+  int off[4] = {0, 0, 0, 0};
+  uint32_t word = 0;
+  for (int k0 = 0; k0 < g.kv; k0 += kDenseBatch) {
+    int32_t v[kDenseBatch];
+#pragma unroll
+    for (int u = 0; u < kDenseBatch; ++u) {
+      uint64_t key;
+      v[u] = kNoRow;
+      if (k0 + u < g.kv) {
+        if (subm_source_key(g, c, off, &key)) v[u] = grid[key];
+        odometer_next(g, off);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kDenseBatch; ++u) {
+      const int k = k0 + u;
+      if (k < g.kv) {
+        const int32_t j = v[u] == kNoRow ? -1 : v[u];
+        if (pf) pf[int64_t(k) * n + r] = j;
+        if (pb) pb[int64_t(g.kv - 1 - k) * n + r] = j;
+        if (j >= 0) word |= 1u << (k & 31);
+        if ((k & 31) == 31 || k == g.kv - 1) {
+          if (words) words[r * mic + (k >> 5)] = word;
+          word = 0;
+        }
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // regular / transpose
 // ---------------------------------------------------------------------------
@@ -494,6 +577,10 @@ size_t sp_pairgen_workspace_size(const sp_geom* g, int64_t n) {
   const bool key64 = need_key64(d);
   if (d.mode == SP_PAIR_SUBM) {
     WsSizerP z;
+    if (subm_dense(d, n)) {
+      z.take<int32_t>(size_t(subm_cells(d)));
+      return z.off;
+    }
     void* ta;
     int32_t* tv;
     int* fl;
@@ -521,13 +608,26 @@ int sp_pairgen_subm(const sp_geom* g, const int32_t* indices, int64_t n, int32_t
   hipStream_t s = as_stream(stream);
   const bool key64 = need_key64(d);
   WsCursor c(ws, ws_bytes);
+  const int mic = (d.kv + 31) / 32;
+  const unsigned blocks = unsigned(cdiv(n, 256));
+  if (subm_dense(d, n)) {
+    const int64_t cells = subm_cells(d);
+    int32_t* grid = c.take<int32_t>(size_t(cells));
+    const int64_t fb = cdiv(cdiv(cells, 4), 256);
+    fill_i32x4<<<unsigned(fb < 4096 ? fb : 4096), 256, 0, s>>>(grid, cells, kNoRow);
+    SP_LAUNCHED();
+    subm_insert_dense<<<blocks, 256, 0, s>>>(indices, n, d, grid);
+    SP_LAUNCHED();
+    subm_probe_dense<<<blocks, 256, 0, s>>>(indices, n, d, grid, pair_fwd, pair_bwd, mask_words,
+                                            mic);
+    SP_LAUNCHED();
+    return SP_OK;
+  }
   void* ta;
   int32_t* tv;
   int* flags;
   uint64_t cap;
   subm_layout(c, n, key64, &ta, &tv, &flags, &cap);
-  const int mic = (d.kv + 31) / 32;
-  const unsigned blocks = unsigned(cdiv(n, 256));
   rc = launch_fill_u64(static_cast<uint64_t*>(ta), int64_t(cap), kEmpty64, s);
   if (rc) return rc;
   if (key64) {

@@ -81,26 +81,22 @@ __global__ __launch_bounds__(kRsThreads) void rs_hist(const Item* __restrict__ i
 }
 
 // Placement of this tile's digits from tile-major histograms (thread d: digit d).
+// The loads go out 32 at a time: each batch is one memory round trip.
 __device__ __forceinline__ uint32_t fused_tile_base(const uint32_t* __restrict__ hist,
                                                     int64_t ntiles, uint32_t* scan_lds) {
+  constexpr int kBatch = 32;
   const uint32_t d = threadIdx.x;
   const int64_t me = blockIdx.x;
   uint32_t total = 0, pre = 0;
-  int64_t b = 0;
-  for (; b + 8 <= ntiles; b += 8) {
-    uint32_t h[8];
+  for (int64_t b = 0; b < ntiles; b += kBatch) {
+    uint32_t h[kBatch];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) h[u] = hist[(b + u) * kRsRadix + d];
+    for (int u = 0; u < kBatch; ++u) h[u] = b + u < ntiles ? hist[(b + u) * kRsRadix + d] : 0u;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < kBatch; ++u) {
       total += h[u];
       pre += b + u < me ? h[u] : 0u;
     }
-  }
-  for (; b < ntiles; ++b) {
-    const uint32_t h = hist[b * kRsRadix + d];
-    total += h;
-    pre += b < me ? h : 0u;
   }
   uint32_t all = 0;
   return block_exclusive_scan<kRsThreads>(total, scan_lds, &all) + pre;

@@ -99,6 +99,41 @@ def test_igemm_pairs_bit_exact(gi, is_train):
     _compare_igemm(res, exp, t, g[6], is_train)
 
 
+def _subm_uses_dense_grid(batch, shape, ks, n):
+    """Whether sp_pairgen_subm takes its dense cell -> row grid (workspace of
+    one int32 per cell) rather than the coordinate hash."""
+    from spconv_triton.pytorch._impl import _lib
+
+    g = _lib.make_geom(_lib.SP_PAIR_SUBM, batch, shape, shape, ks, [1] * len(shape),
+                       [0] * len(shape), [1] * len(shape))
+    return _lib.lib().sp_pairgen_workspace_size(g, n) == batch * int(np.prod(shape)) * 4
+
+
+SUBM_GEOMS = [i for i, g in enumerate(GEOMS) if g[6]]
+
+
+@pytest.mark.parametrize("gi", SUBM_GEOMS)
+def test_subm_dense_and_hash_paths_bit_exact(gi):
+    """Subm tables come from a dense cell -> row grid when the key volume is
+    small next to the number of rows, else from the coordinate hash; both
+    must match the oracle bit for bit.  The same number of points is probed
+    in the geometry's own grid (dense) and in a grid large enough per row for
+    the hash (over 256 cells per row)."""
+    shape, ks, st, pad, dil, op, subm, tr = GEOMS[gi]
+    rng = np.random.default_rng(2000 + gi)
+    n = max(8, int(np.prod(shape)) // 5)
+    big_scale = 8
+    while 3 * int(np.prod(shape)) * big_scale ** len(shape) <= 256 * 3 * n:
+        big_scale *= 2
+    for scale in (1, big_scale):
+        big = [s * scale for s in shape]
+        idx = rand_indices(rng, 3, big, n)
+        assert _subm_uses_dense_grid(3, big, ks, idx.shape[0]) == (scale == 1)
+        g = (big, ks, st, pad, dil, op, subm, tr)
+        res, exp, t = _igemm(idx, 3, g, True)
+        _compare_igemm(res, exp, t, True, True)
+
+
 @pytest.mark.parametrize("gi", [0, 2, 3, 6, 7])
 def test_mask_split_bit_exact(gi):
     g = GEOMS[gi]
