@@ -1,5 +1,11 @@
 // Stable LSD radix sort and the mask-word split/sort entry point.
 //
+// Digits are up to kRsMaxBits = 9 bits wide: a sort over B key bits takes
+// ceil(B / 9) passes with the bits spread evenly over them (27-bit mask words:
+// 3 passes of 9 bits; 32-bit keys: 4 of 8).  A pass costs about the same at
+// 8 or 9 bits, and for these sizes (10^5 - 10^6 items) its cost is mostly
+// latency, so fewer passes is what pays.
+//
 // Tile layout: a workgroup of 256 threads (4 waves) owns a tile of 2048
 // consecutive items, visited in 8 rounds; in round r wave w holds items
 // [r*256 + w*64, +64).  The 32 (round, wave) segments are in item order, so a
@@ -7,9 +13,10 @@
 // local rank.  Global placement of digit d of tile b: all items with a smaller
 // digit plus the items of digit d in tiles before b.  Up to kRsFusedTiles
 // tiles, the histograms are stored tile-major and every scatter workgroup
-// sums them itself (one coalesced 1 KiB row per tile, then a 256-wide block
-// scan), so a pass is two launches; above that they are stored digit-major and
-// a device-wide exclusive scan gives the placements.
+// sums them itself (coalesced rows, 32 tiles per memory round trip, then a
+// block scan), so a pass is two launches; above that they are stored
+// digit-major and a device-wide exclusive scan gives the placements.  The
+// first pass of a row sort generates the row indices itself.
 #include "sp_sort.h"
 
 namespace sp {
@@ -17,9 +24,11 @@ namespace sp {
 constexpr int kRsThreads = 256;
 constexpr int kRsRounds = 8;
 constexpr int kRsTile = kRsThreads * kRsRounds;  // 2048
-constexpr int kRsRadix = 256;
+constexpr int kRsMaxBits = 9;
+constexpr int kRsMaxRadix = 1 << kRsMaxBits;             // 512
 constexpr int kRsSegs = kRsRounds * (kRsThreads / 64);  // 32
-constexpr int64_t kRsFusedTiles = 128;  // per scatter workgroup: 128 KiB of histogram reads
+constexpr int64_t kRsFusedTiles = 128;
+static_assert(kRsTile < 65536, "segment counts are stored as uint16");
 
 struct RowWordDigit {
   const uint32_t* words;
@@ -27,41 +36,54 @@ struct RowWordDigit {
   int w;
   uint32_t andmask;
   int shift;
+  uint32_t dmask;
   __device__ __forceinline__ uint32_t operator()(uint32_t row) const {
-    return ((words[int64_t(row) * mic + w] & andmask) >> shift) & 0xFFu;
+    return ((words[int64_t(row) * mic + w] & andmask) >> shift) & dmask;
   }
 };
 
 struct KeyDigit32 {
   int shift;
-  __device__ __forceinline__ uint32_t operator()(uint32_t k) const { return (k >> shift) & 0xFFu; }
+  uint32_t dmask;
+  __device__ __forceinline__ uint32_t operator()(uint32_t k) const { return (k >> shift) & dmask; }
 };
 
 struct KeyDigit64 {
   int shift;
+  uint32_t dmask;
   __device__ __forceinline__ uint32_t operator()(uint64_t k) const {
-    return uint32_t(k >> shift) & 0xFFu;
+    return uint32_t(k >> shift) & dmask;
   }
 };
 
-// Lanes of the wave holding the same 8-bit digit (restricted to `active`).
-__device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t active) {
+// Lanes of the wave holding the same digit of `db` bits (restricted to `active`).
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t active, int db) {
   uint64_t peers = active;
 #pragma unroll
-  for (int b = 0; b < 8; ++b) {
-    const bool bit = (d >> b) & 1u;
-    const uint64_t m = __ballot(bit);
-    peers &= bit ? m : ~m;
+  for (int b = 0; b < kRsMaxBits; ++b) {
+    if (b < db) {
+      const bool bit = (d >> b) & 1u;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
   }
   return peers;
 }
 
+// Item idx of a pass: in[idx], or idx itself when in is null (the first pass
+// of a row sort).
+template <class Item>
+__device__ __forceinline__ Item rs_item(const Item* __restrict__ in, int64_t idx) {
+  return in ? in[idx] : Item(idx);
+}
+
 template <class Item, class Digit>
 __global__ __launch_bounds__(kRsThreads) void rs_hist(const Item* __restrict__ in, int64_t n,
-                                                     Digit dig, uint32_t* __restrict__ hist,
-                                                     int64_t ntiles) {
-  __shared__ uint32_t cnt[kRsRadix];
-  cnt[threadIdx.x] = 0;
+                                                     Digit dig, int db,
+                                                     uint32_t* __restrict__ hist, int64_t ntiles) {
+  __shared__ uint32_t cnt[kRsMaxRadix];
+  const int R = 1 << db;
+  for (int i = threadIdx.x; i < R; i += kRsThreads) cnt[i] = 0;
   __syncthreads();
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t base = int64_t(blockIdx.x) * kRsTile;
@@ -69,54 +91,81 @@ __global__ __launch_bounds__(kRsThreads) void rs_hist(const Item* __restrict__ i
   for (int r = 0; r < kRsRounds; ++r) {
     const int64_t idx = base + r * kRsThreads + wave * 64 + lane;
     const bool valid = idx < n;
-    const uint32_t d = valid ? dig(in[idx]) : 0u;
-    const uint64_t peers = match_digit(d, __ballot(valid));
+    const uint32_t d = valid ? dig(rs_item(in, idx)) : 0u;
+    const uint64_t peers = match_digit(d, __ballot(valid), db);
     if (valid && (peers & lanemask_lt()) == 0) atomicAdd(&cnt[d], uint32_t(__popcll(peers)));
   }
   __syncthreads();
-  if (ntiles <= kRsFusedTiles)
-    hist[int64_t(blockIdx.x) * kRsRadix + threadIdx.x] = cnt[threadIdx.x];  // [tile][digit]
-  else
-    hist[int64_t(threadIdx.x) * ntiles + blockIdx.x] = cnt[threadIdx.x];  // [digit][tile]
+  for (int i = threadIdx.x; i < R; i += kRsThreads) {
+    if (ntiles <= kRsFusedTiles)
+      hist[int64_t(blockIdx.x) * R + i] = cnt[i];  // [tile][digit]
+    else
+      hist[int64_t(i) * ntiles + blockIdx.x] = cnt[i];  // [digit][tile]
+  }
 }
 
-// Placement of this tile's digits from tile-major histograms (thread d: digit d).
-// The loads go out 32 at a time: each batch is one memory round trip.
-__device__ __forceinline__ uint32_t fused_tile_base(const uint32_t* __restrict__ hist,
-                                                    int64_t ntiles, uint32_t* scan_lds) {
+// Placement of this tile's digits from tile-major histograms, into
+// tile_base[0..R).  Thread t owns digits [t * P, t * P + P), P = R / 256 or 1,
+// read as one contiguous P-word vector per tile (a wave reads 256 or 512
+// consecutive bytes of a histogram row); 32 tiles per memory round trip.
+__device__ __forceinline__ void fused_tile_base(const uint32_t* __restrict__ hist, int64_t ntiles,
+                                                int R, uint32_t* tile_base, uint32_t* scan_lds) {
   constexpr int kBatch = 32;
-  const uint32_t d = threadIdx.x;
   const int64_t me = blockIdx.x;
-  uint32_t total = 0, pre = 0;
-  for (int64_t b = 0; b < ntiles; b += kBatch) {
-    uint32_t h[kBatch];
+  uint32_t tot0 = 0, tot1 = 0, pre0 = 0, pre1 = 0;
+  if (R > kRsThreads) {  // two digits per thread
+    const int d0 = int(threadIdx.x) * 2;
+    for (int64_t b = 0; b < ntiles; b += kBatch) {
+      uint2 h[kBatch];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) h[u] = b + u < ntiles ? hist[(b + u) * kRsRadix + d] : 0u;
+      for (int u = 0; u < kBatch; ++u)
+        h[u] = b + u < ntiles ? *reinterpret_cast<const uint2*>(hist + (b + u) * R + d0)
+                              : make_uint2(0u, 0u);
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      total += h[u];
-      pre += b + u < me ? h[u] : 0u;
+      for (int u = 0; u < kBatch; ++u) {
+        tot0 += h[u].x;
+        tot1 += h[u].y;
+        pre0 += b + u < me ? h[u].x : 0u;
+        pre1 += b + u < me ? h[u].y : 0u;
+      }
     }
+    uint32_t all = 0;
+    const uint32_t run = block_exclusive_scan<kRsThreads>(tot0 + tot1, scan_lds, &all);
+    tile_base[d0] = run + pre0;
+    tile_base[d0 + 1] = run + tot0 + pre1;
+  } else {
+    const int d = int(threadIdx.x);
+    for (int64_t b = 0; b < ntiles; b += 2 * kBatch) {
+      uint32_t h[2 * kBatch];
+#pragma unroll
+      for (int u = 0; u < 2 * kBatch; ++u)
+        h[u] = (b + u < ntiles && d < R) ? hist[(b + u) * R + d] : 0u;
+#pragma unroll
+      for (int u = 0; u < 2 * kBatch; ++u) {
+        tot0 += h[u];
+        pre0 += b + u < me ? h[u] : 0u;
+      }
+    }
+    uint32_t all = 0;
+    const uint32_t run = block_exclusive_scan<kRsThreads>(tot0, scan_lds, &all);
+    if (d < R) tile_base[d] = run + pre0;
   }
-  uint32_t all = 0;
-  return block_exclusive_scan<kRsThreads>(total, scan_lds, &all) + pre;
 }
 
 template <class Item, class Digit>
 __global__ __launch_bounds__(kRsThreads) void rs_scatter(const Item* __restrict__ in,
                                                         Item* __restrict__ out, int64_t n,
-                                                        Digit dig,
+                                                        Digit dig, int db,
                                                         const uint32_t* __restrict__ offsets,
                                                         int64_t ntiles) {
-  __shared__ uint32_t seg[kRsSegs][kRsRadix];
-  __shared__ uint32_t tile_base[kRsRadix];
+  __shared__ __align__(16) uint16_t seg[kRsSegs][kRsMaxRadix];
+  __shared__ uint32_t tile_base[kRsMaxRadix];
   __shared__ uint32_t scan_lds[kRsThreads / 64 + 1];
-  for (int i = threadIdx.x; i < kRsSegs * kRsRadix; i += kRsThreads) (&seg[0][0])[i] = 0;
-  if (ntiles <= kRsFusedTiles)
-    tile_base[threadIdx.x] = fused_tile_base(offsets, ntiles, scan_lds);
-  else
-    tile_base[threadIdx.x] = offsets[int64_t(threadIdx.x) * ntiles + blockIdx.x];
-  __syncthreads();
+  const int R = 1 << db;
+  for (int i = threadIdx.x; i < kRsSegs * kRsMaxRadix / 8; i += kRsThreads)
+    reinterpret_cast<uint4*>(&seg[0][0])[i] = make_uint4(0u, 0u, 0u, 0u);
+  // the tile's items and digits first: their loads overlap the histogram
+  // loads of the placement below
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t base = int64_t(blockIdx.x) * kRsTile;
   Item items[kRsRounds];
@@ -125,22 +174,43 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter(const Item* __restrict_
 #pragma unroll
   for (int r = 0; r < kRsRounds; ++r) {
     const int64_t idx = base + r * kRsThreads + wave * 64 + lane;
+    items[r] = idx < n ? rs_item(in, idx) : Item(0);
+  }
+#pragma unroll
+  for (int r = 0; r < kRsRounds; ++r) {
+    const int64_t idx = base + r * kRsThreads + wave * 64 + lane;
+    digits[r] = idx < n ? dig(items[r]) : 0u;
+  }
+  if (ntiles <= kRsFusedTiles) {
+    // (the barriers of its block scan also order the zeroing of seg before
+    // the segment counts below)
+    fused_tile_base(offsets, ntiles, R, tile_base, scan_lds);
+  } else {
+    for (int i = threadIdx.x; i < R; i += kRsThreads)
+      tile_base[i] = offsets[int64_t(i) * ntiles + blockIdx.x];
+    __syncthreads();
+  }
+#pragma unroll
+  for (int r = 0; r < kRsRounds; ++r) {
+    const int64_t idx = base + r * kRsThreads + wave * 64 + lane;
     const bool valid = idx < n;
-    items[r] = valid ? in[idx] : Item(0);
-    const uint32_t d = valid ? dig(items[r]) : 0u;
-    digits[r] = d;
-    const uint64_t peers = match_digit(d, __ballot(valid));
+    const uint32_t d = digits[r];
+    const uint64_t peers = match_digit(d, __ballot(valid), db);
     const uint64_t below = peers & lanemask_lt();
     ranks[r] = uint32_t(__popcll(below));
-    if (valid && below == 0) seg[r * 4 + wave][d] = uint32_t(__popcll(peers));
+    if (valid && below == 0) seg[r * 4 + wave][d] = uint16_t(__popcll(peers));
   }
   __syncthreads();
-  {
+  // per digit, exclusive scan over the 32 segments (all 32 reads in flight)
+  for (int d = threadIdx.x; d < R; d += kRsThreads) {
+    uint32_t c[kRsSegs];
+#pragma unroll
+    for (int sgi = 0; sgi < kRsSegs; ++sgi) c[sgi] = seg[sgi][d];
     uint32_t run = 0;
-    for (int s = 0; s < kRsSegs; ++s) {
-      const uint32_t c = seg[s][threadIdx.x];
-      seg[s][threadIdx.x] = run;
-      run += c;
+#pragma unroll
+    for (int sgi = 0; sgi < kRsSegs; ++sgi) {
+      seg[sgi][d] = uint16_t(run);
+      run += c[sgi];
     }
   }
   __syncthreads();
@@ -154,34 +224,43 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter(const Item* __restrict_
   }
 }
 
-__global__ void iota_u32(uint32_t* __restrict__ p, int64_t n) {
-  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = uint32_t(i);
-}
-
 struct RsBuffers {
   uint32_t* hist;
   void* scan_ws;
 };
 
-static size_t rs_hist_words(int64_t n) { return size_t(kRsRadix) * size_t(cdiv(n, kRsTile)); }
+static size_t rs_hist_words(int64_t n) {
+  return size_t(kRsMaxRadix) * size_t(cdiv(n, kRsTile));
+}
 
+// One pass over the digit dig (db bits).  in == nullptr: the items are the
+// indices 0..n-1.
 template <class Item, class Digit>
-static int radix_pass(const Item* in, Item* out, int64_t n, Digit dig, const RsBuffers& b,
+static int radix_pass(const Item* in, Item* out, int64_t n, Digit dig, int db, const RsBuffers& b,
                       hipStream_t s) {
   const int64_t ntiles = cdiv(n, kRsTile);
   SP_CHECK_ARG(ntiles <= kMaxGridX, "radix sort: %lld items exceed the grid limit", (long long)n);
-  rs_hist<Item, Digit><<<dim3(unsigned(ntiles)), dim3(kRsThreads), 0, s>>>(in, n, dig, b.hist,
-                                                                          ntiles);
+  rs_hist<Item, Digit><<<dim3(unsigned(ntiles)), dim3(kRsThreads), 0, s>>>(in, n, dig, db,
+                                                                          b.hist, ntiles);
   SP_LAUNCHED();
   if (ntiles > kRsFusedTiles) {
-    int rc = exclusive_scan_u32(b.hist, b.hist, int64_t(kRsRadix) * ntiles, nullptr, b.scan_ws, s);
+    int rc = exclusive_scan_u32(b.hist, b.hist, (int64_t(1) << db) * ntiles, nullptr, b.scan_ws,
+                                s);
     if (rc) return rc;
   }
-  rs_scatter<Item, Digit><<<dim3(unsigned(ntiles)), dim3(kRsThreads), 0, s>>>(in, out, n, dig,
+  rs_scatter<Item, Digit><<<dim3(unsigned(ntiles)), dim3(kRsThreads), 0, s>>>(in, out, n, dig, db,
                                                                              b.hist, ntiles);
   SP_LAUNCHED();
   return SP_OK;
+}
+
+// Digit widths of a sort over `bits` key bits: ceil(bits / 9) passes with the
+// bits spread evenly (widths differ by at most one, wider first).
+static int digit_plan(int bits, int* widths) {
+  if (bits <= 0) return 0;
+  const int passes = (bits + kRsMaxBits - 1) / kRsMaxBits;
+  for (int i = 0; i < passes; ++i) widths[i] = bits / passes + (i < bits % passes ? 1 : 0);
+  return passes;
 }
 
 template <class W>
@@ -198,6 +277,11 @@ size_t sort_rows_ws_bytes(int64_t n) {
   return z.off;
 }
 
+__global__ void iota_u32(uint32_t* __restrict__ p, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = uint32_t(i);
+}
+
 int sort_rows_by_words(const uint32_t* words, int64_t n, int mic, int kv, uint32_t split,
                        uint32_t** perm_out, void* ws, hipStream_t stream) {
   WsCursor c(ws, ~size_t(0));
@@ -206,8 +290,7 @@ int sort_rows_by_words(const uint32_t* words, int64_t n, int mic, int kv, uint32
   RsBuffers bufs;
   bufs.hist = c.take<uint32_t>(rs_hist_words(n));
   bufs.scan_ws = c.take<char>(scan_workspace_bytes(int64_t(rs_hist_words(n))));
-  iota_u32<<<dim3(unsigned(cdiv(n, 256))), dim3(256), 0, stream>>>(a, n);
-  SP_LAUNCHED();
+  bool first = true;  // the first pass reads the identity permutation implicitly
   for (int w = 0; w < mic; ++w) {
     int bits = (w < mic - 1) ? 32 : kv - 32 * (mic - 1);
     uint32_t andmask = 0xFFFFFFFFu;
@@ -216,14 +299,24 @@ int sort_rows_by_words(const uint32_t* words, int64_t n, int mic, int kv, uint32
       const int top = split ? 32 - __builtin_clz(split) : 0;
       bits = bits < top ? bits : top;
     }
-    for (int shift = 0; shift < bits; shift += 8) {
-      RowWordDigit d{words, mic, w, andmask, shift};
-      int rc = radix_pass(a, b, n, d, bufs, stream);
+    int widths[8];
+    const int passes = digit_plan(bits, widths);
+    int shift = 0;
+    for (int i = 0; i < passes; ++i) {
+      RowWordDigit d{words, mic, w, andmask, shift, (1u << widths[i]) - 1u};
+      int rc = radix_pass(first ? static_cast<const uint32_t*>(nullptr) : a, b, n, d, widths[i],
+                          bufs, stream);
       if (rc) return rc;
+      first = false;
+      shift += widths[i];
       uint32_t* t = a;
       a = b;
       b = t;
     }
+  }
+  if (first) {  // nothing to sort by: the identity permutation
+    iota_u32<<<dim3(unsigned(cdiv(n, 256))), dim3(256), 0, stream>>>(a, n);
+    SP_LAUNCHED();
   }
   *perm_out = a;
   return SP_OK;
@@ -250,9 +343,13 @@ static int sort_keys_impl(Item* keys, Item* tmp, int64_t n, int bits, Item** res
   bufs.scan_ws = c.take<char>(scan_workspace_bytes(int64_t(rs_hist_words(n))));
   Item* a = keys;
   Item* b = tmp;
-  for (int shift = 0; shift < bits; shift += 8) {
-    int rc = radix_pass(a, b, n, Digit{shift}, bufs, stream);
+  int widths[8];
+  const int passes = digit_plan(bits, widths);
+  int shift = 0;
+  for (int i = 0; i < passes; ++i) {
+    int rc = radix_pass(a, b, n, Digit{shift, (1u << widths[i]) - 1u}, widths[i], bufs, stream);
     if (rc) return rc;
+    shift += widths[i];
     Item* t = a;
     a = b;
     b = t;
