@@ -24,19 +24,20 @@
 //        for every (item, row).
 //      - B: the four waves share the tile's item list, and each item's 4 KiB
 //        weight slab is loaded once per workgroup (16 bytes per thread) into a
-//        3-slot LDS ring, one barrier per item.
-//    Tiles whose distinct rows do not fit in LDS (the plan's overflow list)
-//    are left to the direct kernel.
+//        4-slot LDS ring, one barrier per two items.
+//    Tiles whose distinct rows do not fit in LDS (the plan's overflow tiles)
+//    take the direct path inside the same kernel.
 //  * gather_gemm_direct: fragments are gathered straight from global memory
 //    (A) and B is read through L1 by every wave.  It runs every tile of an
-//    unplanned call, or only the overflow tiles of a planned one, and builds
-//    its per-wave item tables from the pair table itself.
+//    unplanned call (its body, direct_tile, also serves the overflow tiles of
+//    a planned one), and builds its per-wave item tables from the pair table
+//    itself.
 //
 // Both pipelines keep per-item work to loads and MFMAs: B offsets and A
-// addresses are precomputed per item, and the item lists end with kPad
-// padding items (zero row, out-of-range B), so the loops run in whole groups of
-// 3 items and read ahead without per-item conditions.  Padding items multiply
-// zeros, which leaves every sum unchanged.  Raw buffer instructions make global
+// addresses are precomputed per item, and the item lists end with padding
+// items (zero row, out-of-range B), so the loops run in whole groups (3 items
+// direct, 4 staged) and read ahead without per-item conditions.  Padding items
+// multiply zeros, which leaves every sum unchanged.  Raw buffer instructions make global
 // loads branch-free (an offset past the buffer's size reads zeros, a store
 // there is dropped), and sched_barrier keeps loads issued ahead of the MFMAs
 // that consume them, so the compiler's load counters stay exact.

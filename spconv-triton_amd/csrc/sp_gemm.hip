@@ -5,11 +5,11 @@
 //
 //   out[m, n] = bias[n] + sum_k sum_r A[pairs[k, m], r] * B[k][n][r]
 //
-// The kernel itself (sp_gather_gemm.h): a workgroup owns 256 output rows x 64
-// output columns, a wave 64 x 64 as 4 x 4 tiles of 16x16 MFMAs.  Gathered A
-// rows come from LDS, where the tile's distinct source rows are staged once
-// per K-step using a gather plan (sp_plan.h), or straight from global memory
-// when there is no plan.  B (the weights) is relaid once into [k][r / V][n][V]
+// The kernels themselves (sp_gather_gemm.h): a workgroup owns 256 output rows
+// x 64 output columns, a wave 64 x 64 as 2 x 2 tiles of 32x32 MFMAs.  Gathered
+// A rows come from LDS, where the tile's distinct source rows are staged once
+// per 64-byte reduction chunk using a gather plan (sp_plan.h), or straight
+// from global memory when there is no plan (or the tile's rows do not fit).  B (the weights) is relaid once into [k][r / V][n][V]
 // (V elements = 16 bytes), which makes every B operand load a coalesced 1 KiB
 // read.  Any assignment of reduction indices to (MFMA step, lane group,
 // element) is valid as long as A and B use the same one.
