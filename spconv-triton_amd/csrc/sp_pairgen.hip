@@ -355,6 +355,135 @@ static void conv_layout(W& w, const GeomDev& g, int64_t n, bool key64, ConvWs* o
   }
 }
 
+// ---- regular / transposed convs on an occupancy bitmap ------------------------
+// With int32 keys and an output key volume of at most kBitmapCellsPerRow cells
+// per input row, one bit per output cell replaces the hash, the key sort and
+// the ranking.  Candidates set their cell's bit; an exclusive scan of the
+// 32-bit words' popcounts gives each word's first rank; a key's output row is
+// that prefix plus the popcount of its word's lower bits, i.e. its rank in
+// ascending key order (torch.unique's order, as the hash path's sort gives).
+// The set bits, read in word order, are the sorted unique keys themselves.
+constexpr int64_t kBitmapCellsPerRow = 4096;
+
+static bool conv_bitmap(const GeomDev& g, int64_t n, bool key64) {
+  if (key64) return false;
+  const double vol = double(g.batch) * double(prod_shape(g.out_shape, g.ndim));
+  return vol <= double(kBitmapCellsPerRow) * double(n);
+}
+
+struct BitmapWs {
+  uint32_t* bits;    // [words] occupancy, bit key % 32 of word key / 32
+  uint32_t* prefix;  // [words] set bits in the words before
+  uint32_t* total;   // number of set bits
+  void* scan_ws;
+  int64_t words;
+};
+
+template <class W>
+static void bitmap_layout(W& w, const GeomDev& g, BitmapWs* out) {
+  const int64_t words = cdiv(g.batch * prod_shape(g.out_shape, g.ndim), 32);
+  auto* bits = w.template take<uint32_t>(size_t(words));
+  auto* prefix = w.template take<uint32_t>(size_t(words));
+  auto* total = w.template take<uint32_t>(64);
+  void* sws = w.template take<char>(scan_workspace_bytes(words));
+  if (out) *out = BitmapWs{bits, prefix, total, sws, words};
+}
+
+// One thread per input row j: set the bits of its candidate outputs.  The kv
+// candidates of a row come in key order along the fastest dimension, so runs
+// in one word are ORed together before the atomic.
+__global__ __launch_bounds__(256) void conv_mark(const int32_t* __restrict__ idx, int64_t n,
+                                                 GeomDev g, uint32_t* __restrict__ bits) {
+  const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  const Coord c = load_coord(idx, j, g);
+  int off[4] = {0, 0, 0, 0};
+  uint32_t cw = 0, cb = 0;  // pending word and its bits (cb == 0: none)
+  for (int k = 0; k < g.kv; ++k) {
+    uint64_t key;
+    if (candidate_key(g, c, off, &key)) {
+      const uint32_t w = uint32_t(key >> 5), b = 1u << uint32_t(key & 31u);
+      if (cb != 0 && w != cw) {
+        atomicOr(&bits[cw], cb);
+        cb = 0;
+      }
+      cw = w;
+      cb |= b;
+    }
+    odometer_next(g, off);
+  }
+  if (cb != 0) atomicOr(&bits[cw], cb);
+}
+
+__global__ __launch_bounds__(256) void popc_words(const uint32_t* __restrict__ bits, int64_t words,
+                                                  uint32_t* __restrict__ out) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < words) out[i] = uint32_t(__popc(bits[i]));
+}
+
+// Output row of a marked key.
+__device__ __forceinline__ int64_t bitmap_rank(const uint32_t* __restrict__ bits,
+                                               const uint32_t* __restrict__ prefix, uint64_t key) {
+  const uint64_t w = key >> 5;
+  const uint32_t below = bits[w] & ((1u << uint32_t(key & 31u)) - 1u);
+  return int64_t(prefix[w]) + __popc(below);
+}
+
+// conv_fill with the bitmap's ranks.
+__global__ __launch_bounds__(256) void conv_fill_bitmap(
+    const int32_t* __restrict__ idx, int64_t n, GeomDev g, const uint32_t* __restrict__ bits,
+    const uint32_t* __restrict__ prefix, int64_t n_keep, int32_t* __restrict__ pf,
+    int32_t* __restrict__ pb, uint32_t* __restrict__ words, int mic) {
+  const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (j >= n) return;
+  const Coord c = load_coord(idx, j, g);
+  int off[4] = {0, 0, 0, 0};
+  uint32_t word = 0;
+  for (int k = 0; k < g.kv; ++k) {
+    uint64_t key;
+    int32_t r = -1;
+    if (candidate_key(g, c, off, &key)) {
+      const int64_t rank = bitmap_rank(bits, prefix, key);
+      r = rank < n_keep ? int32_t(rank) : -1;
+    }
+    if (r >= 0) {
+      if (pf) pf[int64_t(k) * n_keep + r] = int32_t(j);
+      word |= 1u << (k & 31);
+    }
+    if (pb) pb[int64_t(k) * n + j] = r;
+    if ((k & 31) == 31 || k == g.kv - 1) {
+      if (words) words[j * mic + (k >> 5)] = word;
+      word = 0;
+    }
+    odometer_next(g, off);
+  }
+}
+
+// Output coordinates of the kept rows: one thread per bitmap word, its set
+// bits in order (rows prefix[w], prefix[w] + 1, ...).
+__global__ __launch_bounds__(256) void emit_bitmap_keys(const uint32_t* __restrict__ bits,
+                                                        const uint32_t* __restrict__ prefix,
+                                                        int64_t nwords, GeomDev g, int64_t n_keep,
+                                                        int32_t* __restrict__ out) {
+  const int64_t w = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (w >= nwords) return;
+  uint32_t m = bits[w];
+  int64_t r = prefix[w];
+  while (m != 0 && r < n_keep) {
+    const int b = __ffs(m) - 1;
+    m &= m - 1u;
+    uint64_t rem = uint64_t(w) * 32u + uint64_t(b);
+    int32_t* o = out + r * (g.ndim + 1);
+    for (int d = g.ndim - 1; d >= 0; --d) {
+      const uint64_t sd = uint64_t(g.out_shape[d]);
+      o[d + 1] = int32_t(rem % sd);
+      rem /= sd;
+    }
+    o[0] = int32_t(rem);
+    ++r;
+  }
+}
+
 // Sizer variant returning nulls (the WsSizer::take returns void).
 struct WsSizerP {
   size_t off = 0;
@@ -589,6 +718,10 @@ size_t sp_pairgen_workspace_size(const sp_geom* g, int64_t n) {
     return z.off;
   }
   WsSizerP z;
+  if (conv_bitmap(d, n, key64)) {
+    bitmap_layout(z, d, nullptr);
+    return z.off;
+  }
   conv_layout(z, d, n, key64, nullptr);
   return z.off;
 }
@@ -662,6 +795,27 @@ int sp_pairgen_conv_build(const sp_geom* g, const int32_t* indices, int64_t n, v
   hipStream_t s = as_stream(stream);
   const bool key64 = need_key64(d);
   WsCursor c(ws, ws_bytes);
+  if (conv_bitmap(d, n, key64)) {
+    BitmapWs b;
+    bitmap_layout(c, d, &b);
+    const int64_t fb = cdiv(cdiv(b.words, 4), 256);
+    fill_i32x4<<<unsigned(fb < 4096 ? fb : 4096), 256, 0, s>>>(
+        reinterpret_cast<int32_t*>(b.bits), b.words, 0);
+    SP_LAUNCHED();
+    conv_mark<<<unsigned(cdiv(n, 256)), 256, 0, s>>>(indices, n, d, b.bits);
+    SP_LAUNCHED();
+    const int64_t pbk = cdiv(b.words, 256);
+    SP_CHECK_ARG(pbk <= kMaxGridX, "pairgen: output volume too large");
+    popc_words<<<unsigned(pbk), 256, 0, s>>>(b.bits, b.words, b.prefix);
+    SP_LAUNCHED();
+    rc = exclusive_scan_u32(b.prefix, b.prefix, b.words, b.total, b.scan_ws, s);
+    if (rc) return rc;
+    uint32_t h = 0;
+    SP_HIP(hipMemcpyAsync(&h, b.total, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    SP_HIP(hipStreamSynchronize(s));
+    *n_out = int64_t(h);
+    return SP_OK;
+  }
   ConvWs w;
   conv_layout(c, d, n, key64, &w);
   SP_HIP(hipMemsetAsync(w.flags, 0, 256, s));
@@ -740,13 +894,25 @@ int sp_pairgen_conv_fill(const sp_geom* g, const int32_t* indices, int64_t n, co
   hipStream_t s = as_stream(stream);
   const bool key64 = need_key64(d);
   WsCursor c(const_cast<void*>(ws), ws_bytes);
-  ConvWs w;
-  conv_layout(c, d, n, key64, &w);
   const int mic = (d.kv + 31) / 32;
   if (pair_fwd) {
     rc = launch_fill_i32(pair_fwd, int64_t(d.kv) * n_keep, -1, s);
     if (rc) return rc;
   }
+  if (conv_bitmap(d, n, key64)) {
+    BitmapWs b;
+    bitmap_layout(c, d, &b);
+    conv_fill_bitmap<<<unsigned(cdiv(n, 256)), 256, 0, s>>>(indices, n, d, b.bits, b.prefix,
+                                                            n_keep, pair_fwd, pair_bwd,
+                                                            mask_words_bwd, mic);
+    SP_LAUNCHED();
+    emit_bitmap_keys<<<unsigned(cdiv(b.words, 256)), 256, 0, s>>>(b.bits, b.prefix, b.words, d,
+                                                                  n_keep, out_indices);
+    SP_LAUNCHED();
+    return SP_OK;
+  }
+  ConvWs w;
+  conv_layout(c, d, n, key64, &w);
   const unsigned blocks = unsigned(cdiv(n, 256));
   const unsigned rb = unsigned(cdiv(n_keep, 256));
   if (key64) {

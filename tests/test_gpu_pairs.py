@@ -110,6 +110,57 @@ def _subm_uses_dense_grid(batch, shape, ks, n):
 
 
 SUBM_GEOMS = [i for i, g in enumerate(GEOMS) if g[6]]
+CONV_GEOMS = [i for i, g in enumerate(GEOMS) if not g[6]]
+
+
+def _align256(v):
+    return (v + 255) // 256 * 256
+
+
+def _conv_uses_bitmap(batch, g, n):
+    """Whether sp_pairgen_conv_build takes its occupancy-bitmap path (int32
+    keys, at most 4096 output cells per input row): its workspace is then
+    the bitmap, the word prefix, a counter and the scan's chunk sums."""
+    from spconv_triton.pytorch._impl import _lib, pairs as P
+
+    shape, ks, st, pad, dil, op, subm, tr = g
+    out_shape = P._check_and_shape(torch.zeros(1, len(shape) + 1), shape, ks, st, pad, dil, op,
+                                   False, tr)
+    words = -(-batch * int(np.prod(out_shape)) // 32)
+    w4 = words * 4
+    size = _align256(_align256(_align256(w4) + w4) + 256) + _align256(-(-words // 4096) * 4)
+    mode = _lib.SP_PAIR_TRANSPOSE if tr else _lib.SP_PAIR_REGULAR
+    geom = _lib.make_geom(mode, batch, shape, out_shape, ks, st, pad, dil)
+    return _lib.lib().sp_pairgen_workspace_size(geom, n) == size
+
+
+@pytest.mark.parametrize("gi", CONV_GEOMS)
+def test_conv_bitmap_and_hash_paths_bit_exact(gi):
+    """Regular / transposed tables come from an occupancy bitmap of the
+    output keys when the keys are int32 and the output volume is small next
+    to the number of rows, else from the coordinate hash and a key sort; both
+    must match the oracle bit for bit (output rows in ascending key order)."""
+    shape, ks, st, pad, dil, op, subm, tr = GEOMS[gi]
+    rng = np.random.default_rng(3000 + gi)
+    n = max(8, int(np.prod(shape)) // 5)
+    from spconv_triton.pytorch._impl import pairs as P
+
+    def out_volume(sc):
+        big = [x * sc for x in shape]
+        return int(np.prod(P._check_and_shape(torch.zeros(1, len(shape) + 1), big, ks, st, pad,
+                                              dil, op, False, tr)))
+
+    scale = 8
+    while 3 * out_volume(scale) <= 4096 * 3 * n:
+        scale *= 2
+    for s_ in (1, scale):
+        big = [x * s_ for x in shape]
+        g = (big, ks, st, pad, dil, op, subm, tr)
+        idx = rand_indices(rng, 3, big, n)
+        assert _conv_uses_bitmap(3, g, idx.shape[0]) == (s_ == 1)
+        for is_train in (True, False):
+            res, exp, t = _igemm(idx, 3, g, is_train)
+            _compare_igemm(res, exp, t, False, is_train)
 
 
 @pytest.mark.parametrize("gi", SUBM_GEOMS)
