@@ -142,63 +142,128 @@ __device__ __forceinline__ typename Mfma<T>::frag load_frag_vec(const T* p) {
 // ---------------------------------------------------------------------------
 // weight gradient
 // ---------------------------------------------------------------------------
-constexpr int kWgP = 64;  // pairs per LDS stage
+// dW[n, k, c] = sum over the pairs (i, o) of offset k of X[i, c] * G[o, n]:
+// per offset a GEMM whose reduction runs over that offset's compacted pair
+// list.  A workgroup owns (offset k, a contiguous share of its pairs, a
+// 64 x 64 block of (c, n)); each wave a 32 x 32 block.  The MFMA operands
+// need the pair index as the reduction index, i.e. X and G transposed, so the
+// rows gathered for a stage of kWgStage pairs are written to LDS as
+// [channel][pair] (two pairs per 32-bit write) and read back as 16-byte
+// fragments.  Gathers are 16-byte vector loads; the next stage's rows and the
+// pair indices two stages ahead are in flight while the stage's MFMAs run.
+// fp32 partials per share are summed in a fixed order by wgrad_reduce
+// (deterministic, no atomics).
+constexpr int kWgStage = 128;  // pairs per LDS stage
 
-template <typename T>
+template <typename T, bool VEC>
 __global__ __launch_bounds__(256) void wgrad_partial(
     const T* __restrict__ X, int64_t n_in, const T* __restrict__ G, int64_t n_out, int C, int K,
     int kv, const int32_t* __restrict__ in_rows, const int32_t* __restrict__ out_rows,
-    const int32_t* __restrict__ counts, int64_t stride, int splits, float* __restrict__ part) {
+    const int32_t* __restrict__ counts, int64_t stride, int splits, float* __restrict__ part,
+    uint32_t x_bytes, uint32_t g_bytes) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
   constexpr int V = MF::V;
   constexpr int KSTEP = MF::KSTEP;
-  constexpr int PITCH = kWgP + V;  // row pitch in elements (keeps 16-byte alignment)
+  constexpr uint32_t ES = sizeof(T);
+  constexpr int PITCH = kWgStage + V;  // row pitch in elements (rows stay 16-byte aligned)
+  constexpr int NV = 16 / V;           // vectors per thread, tensor and pair (16 channels)
   __shared__ __align__(16) T Xs[64][PITCH];
   __shared__ __align__(16) T Gs[64][PITCH];
 
   const int k = blockIdx.x / splits;
   const int split = blockIdx.x % splits;
   const int c0 = blockIdx.y * 64, n0 = blockIdx.z * 64;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
   const int h = lane >> 5, l32 = lane & 31;
   const int ctile = (wave >> 1) * 32, ntile = (wave & 1) * 32;
+  // staging role: pairs 2 pp and 2 pp + 1 of a stage, channels 16 q .. 16 q + 15
+  const int pp = tid & 63, q = tid >> 6;
 
   const int64_t cnt = counts[k];
   const int64_t chunk = (cnt + splits - 1) / splits;
   const int64_t p_lo = split * chunk;
   const int64_t p_hi = p_lo + chunk < cnt ? p_lo + chunk : cnt;
 
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(X, x_bytes);
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(G, g_bytes);
+  const int32_t* ir = in_rows + int64_t(k) * stride;
+  const int32_t* orow = out_rows + int64_t(k) * stride;
+
+  // pair indices of stage s0 (-1 past the share's end)
+  auto load_idx = [&](int64_t s0, int32_t (&iv)[2], int32_t (&ov)[2]) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int64_t p = s0 + 2 * pp + e;
+      const bool ok = p < p_hi;
+      const int32_t i = ok ? ir[ok ? p : 0] : -1;
+      const int32_t o = ok ? orow[ok ? p : 0] : -1;
+      iv[e] = (i >= 0 && i < n_in) ? i : -1;
+      ov[e] = (o >= 0 && o < n_out) ? o : -1;
+    }
+  };
+  auto row_off = [&](int32_t r, int ch, int width, int dim) -> uint32_t {
+    return (r >= 0 && ch < dim) ? uint32_t((int64_t(r) * width + ch) * ES) : kOob;
+  };
+  auto load_rows = [&](const int32_t (&iv)[2], const int32_t (&ov)[2], frag (&xv)[2][NV],
+                       frag (&gv)[2][NV]) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int cx = c0 + q * 16 + j * V, nx = n0 + q * 16 + j * V;
+        if (VEC) {
+          xv[e][j] = buf_frag<T>(rx, row_off(iv[e], cx, C, C));
+          gv[e][j] = buf_frag<T>(rg, row_off(ov[e], nx, K, K));
+        } else {
+          xv[e][j] = buf_frag_elems<T>(rx, iv[e] >= 0 ? uint32_t(int64_t(iv[e]) * C * ES) : kOob,
+                                       cx, C);
+          gv[e][j] = buf_frag_elems<T>(rg, ov[e] >= 0 ? uint32_t(int64_t(ov[e]) * K * ES) : kOob,
+                                       nx, K);
+        }
+      }
+  };
+  // channel-major LDS rows: both pairs' values of a channel in one write
+  using T2 = __attribute__((ext_vector_type(2))) T;
+  auto put_rows = [&](const frag (&xv)[2][NV], const frag (&gv)[2][NV]) {
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+      for (int t = 0; t < V; ++t) {
+        const int c = q * 16 + j * V + t;
+        const T2 xp = {xv[0][j][t], xv[1][j][t]};
+        const T2 gp = {gv[0][j][t], gv[1][j][t]};
+        *reinterpret_cast<T2*>(&Xs[c][2 * pp]) = xp;
+        *reinterpret_cast<T2*>(&Gs[c][2 * pp]) = gp;
+      }
+  };
+
   floatx16 acc;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.f;
 
-  constexpr int VPR = 64 / V;  // vectors per 64-channel row
-  for (int64_t p0 = p_lo; p0 < p_hi; p0 += kWgP) {
+  int32_t iv[2], ov[2], iv2[2], ov2[2];
+  frag xv[2][NV], gv[2][NV];
+  load_idx(p_lo, iv, ov);
+  load_rows(iv, ov, xv, gv);
+  load_idx(p_lo + kWgStage, iv2, ov2);
+  for (int64_t s0 = p_lo; s0 < p_hi; s0 += kWgStage) {
+    __syncthreads();  // the previous stage's fragments are read
+    put_rows(xv, gv);
     __syncthreads();
-    for (int v = threadIdx.x; v < kWgP * VPR; v += 256) {
-      const int prow = v / VPR, cv = v % VPR;
-      const int64_t p = p0 + prow;
-      int32_t i = -1, o = -1;
-      if (p < p_hi) {
-        i = in_rows[int64_t(k) * stride + p];
-        o = out_rows[int64_t(k) * stride + p];
-        if (i >= n_in) i = -1;
-        if (o >= n_out) o = -1;
-      }
+    // next stage's rows and the indices after it, in flight during the MFMAs
 #pragma unroll
-      for (int e = 0; e < V; ++e) {
-        const int c = c0 + cv * V + e;
-        const int n = n0 + cv * V + e;
-        Xs[cv * V + e][prow] = (i >= 0 && c < C) ? X[int64_t(i) * C + c] : T(0.f);
-        Gs[cv * V + e][prow] = (o >= 0 && n < K) ? G[int64_t(o) * K + n] : T(0.f);
-      }
+    for (int e = 0; e < 2; ++e) {
+      iv[e] = iv2[e];
+      ov[e] = ov2[e];
     }
-    __syncthreads();
+    load_rows(iv, ov, xv, gv);
+    load_idx(s0 + 2 * kWgStage, iv2, ov2);
 #pragma unroll
-    for (int s = 0; s < kWgP; s += KSTEP) {
-      const frag a = *reinterpret_cast<const frag*>(&Xs[ctile + l32][s + h * V]);
-      const frag b = *reinterpret_cast<const frag*>(&Gs[ntile + l32][s + h * V]);
+    for (int st = 0; st < kWgStage; st += KSTEP) {
+      const frag a = *reinterpret_cast<const frag*>(&Xs[ctile + l32][st + h * V]);
+      const frag b = *reinterpret_cast<const frag*>(&Gs[ntile + l32][st + h * V]);
       MF::mma(a, b, acc);
     }
   }
@@ -549,30 +614,29 @@ int sp_conv_wgrad(const void* x, int64_t n_in, const void* g, int64_t n_out, int
   float* part = static_cast<float*>(ws);
   const int64_t gx = kv * splits;
   SP_CHECK_ARG(gx <= kMaxGridX, "wgrad: grid too large");
+  const int64_t es = dtype == SP_F32 ? 4 : 2;
+  const int64_t xb = n_in * C * es, gb = n_out * K * es;
+  if (xb >= int64_t(kOob) || gb >= int64_t(kOob))
+    return set_error(SP_ERR_UNSUPPORTED, "wgrad: features exceed 4 GiB");
+  // 16-byte row gathers need whole vectors per row and aligned bases
+  const int v = vec_of(dtype);
+  const bool vec = C % v == 0 && K % v == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(g) % 16 == 0;
   dim3 grid(unsigned(gx), unsigned(cdiv(C, 64)), unsigned(cdiv(K, 64)));
   const int64_t tot = K * kv * C;
   const unsigned rb = unsigned(cdiv(tot, 256));
+  auto run = [&](auto tag) {
+    using T = decltype(tag);
+    auto kern = vec ? wgrad_partial<T, true> : wgrad_partial<T, false>;
+    kern<<<grid, 256, 0, s>>>(static_cast<const T*>(x), n_in, static_cast<const T*>(g), n_out,
+                              int(C), int(K), int(kv), in_rows, out_rows, counts, row_stride,
+                              splits, part, uint32_t(xb), uint32_t(gb));
+    wgrad_reduce<T><<<rb, 256, 0, s>>>(part, splits, tot, static_cast<T*>(dw));
+  };
   switch (dtype) {
-    case SP_F16:
-      wgrad_partial<_Float16><<<grid, 256, 0, s>>>(
-          static_cast<const _Float16*>(x), n_in, static_cast<const _Float16*>(g), n_out,
-          int(C), int(K), int(kv), in_rows, out_rows, counts, row_stride, splits, part);
-      SP_LAUNCHED();
-      wgrad_reduce<_Float16><<<rb, 256, 0, s>>>(part, splits, tot, static_cast<_Float16*>(dw));
-      break;
-    case SP_BF16:
-      wgrad_partial<__bf16><<<grid, 256, 0, s>>>(
-          static_cast<const __bf16*>(x), n_in, static_cast<const __bf16*>(g), n_out, int(C),
-          int(K), int(kv), in_rows, out_rows, counts, row_stride, splits, part);
-      SP_LAUNCHED();
-      wgrad_reduce<__bf16><<<rb, 256, 0, s>>>(part, splits, tot, static_cast<__bf16*>(dw));
-      break;
-    default:
-      wgrad_partial<float><<<grid, 256, 0, s>>>(
-          static_cast<const float*>(x), n_in, static_cast<const float*>(g), n_out, int(C),
-          int(K), int(kv), in_rows, out_rows, counts, row_stride, splits, part);
-      SP_LAUNCHED();
-      wgrad_reduce<float><<<rb, 256, 0, s>>>(part, splits, tot, static_cast<float*>(dw));
+    case SP_F16: run(_Float16{}); break;
+    case SP_BF16: run(__bf16{}); break;
+    default: run(float{});
   }
   SP_LAUNCHED();
   return SP_OK;
