@@ -227,10 +227,52 @@ def native_pairs(indices, batch_size, spatial_shape, ksize, stride, padding, dil
     return t.out_inds, pair, npl
 
 
-def igemm_pairs(indices, batch_size, spatial_shape, ksize, stride, padding, dilation,
-                out_padding, subm, transpose, is_train, is_mask_split, do_sort=True,
-                num_out_act_bound=-1):
-    """Implicit-GEMM tables (reference ``pairs.py:281-426``), the same 9-tuple."""
+class DeferredMaskSplits:
+    """The sorted mask splits of one implicit-GEMM rulebook, computed on first use.
+
+    The gather-GEMM skips the offsets a tile has no pair for by itself and never
+    reads the masks, so a rulebook that a module builds for its own use keeps
+    only what the masks are made from: the mask words where pair generation
+    wrote them in passing (subm forward, regular/transposed backward), else the
+    gather table.  ``get()`` runs the sorts the first time the values are asked
+    for and returns what the eager ``igemm_pairs`` returns.
+    """
+
+    def __init__(self, words_fwd: torch.Tensor | None, pair_fwd: torch.Tensor,
+                 words_bwd: torch.Tensor | None, kv: int, masks, do_sort: bool):
+        self._args = (words_fwd, pair_fwd, words_bwd, kv, masks, do_sort)
+        self._stream = torch.cuda.current_stream(pair_fwd.device)
+        self._value = None
+
+    def get(self):
+        """(pair_mask_fwd_splits, pair_mask_bwd_splits, mask_argsort_fwd_splits,
+        mask_argsort_bwd_splits)."""
+        if self._value is None:
+            words_fwd, pair_fwd, words_bwd, kv, masks, do_sort = self._args
+            cur = torch.cuda.current_stream(pair_fwd.device)
+            if cur != self._stream:
+                # the words and the table were written on the build stream
+                cur.wait_stream(self._stream)
+                for w in (words_fwd, words_bwd):
+                    if w is not None:
+                        w.record_stream(cur)
+            if words_fwd is None:
+                words_fwd = mask_words(pair_fwd)
+            pm_fwd, ma_fwd = sort_mask_words(words_fwd, kv, masks, do_sort)
+            if words_bwd is not None:
+                pm_bwd, ma_bwd = sort_mask_words(words_bwd, kv, masks, do_sort)
+            else:
+                pm_bwd, ma_bwd = [], []
+            self._value = (pm_fwd, pm_bwd, ma_fwd, ma_bwd)
+            self._args = None
+        return self._value
+
+
+def igemm_rulebook(indices, batch_size, spatial_shape, ksize, stride, padding, dilation,
+                   out_padding, subm, transpose, is_train, is_mask_split, do_sort=True,
+                   num_out_act_bound=-1):
+    """``igemm_pairs`` with the mask sorts deferred: returns (the 9-tuple with
+    empty mask-split lists, a ``DeferredMaskSplits`` that yields them)."""
     kv = _prod(ksize)
     need_bwd = bool(is_train)
     bound = num_out_act_bound if not subm else -1
@@ -241,20 +283,28 @@ def igemm_pairs(indices, batch_size, spatial_shape, ksize, stride, padding, dila
         raise AssertionError("Not Implemented")
     t = _generate(indices, batch_size, spatial_shape, ksize, stride, padding, dilation,
                   out_padding, subm, transpose, want_fwd=True, want_bwd=need_bwd,
-                  want_words_fwd=True, want_words_bwd=need_bwd and not subm,
+                  want_words_fwd=subm, want_words_bwd=need_bwd and not subm,
                   num_out_act_bound=bound)
     device = t.pair_fwd.device
     npl = torch.zeros((kv,), dtype=torch.int32, device=device)
     masks = split_masks(kv, is_mask_split)
-    pm_fwd, ma_fwd = sort_mask_words(t.words_fwd, kv, masks, do_sort)
-    if is_train and not subm:
-        pm_bwd, ma_bwd = sort_mask_words(t.words_bwd, kv, masks, do_sort)
-    else:
-        pm_bwd, ma_bwd = [], []
+    # t.words_bwd exists for a regular/transposed training rulebook only
+    deferred = DeferredMaskSplits(t.words_fwd, t.pair_fwd, t.words_bwd, kv, masks, do_sort)
     pb = t.pair_bwd if need_bwd else torch.Tensor()
     if subm:
-        return (indices, npl, t.pair_fwd, pb, pm_fwd, [], ma_fwd, [], masks)
-    return (t.out_inds, npl, t.pair_fwd, pb, pm_fwd, pm_bwd, ma_fwd, ma_bwd, masks)
+        return (indices, npl, t.pair_fwd, pb, [], [], [], [], masks), deferred
+    return (t.out_inds, npl, t.pair_fwd, pb, [], [], [], [], masks), deferred
+
+
+def igemm_pairs(indices, batch_size, spatial_shape, ksize, stride, padding, dilation,
+                out_padding, subm, transpose, is_train, is_mask_split, do_sort=True,
+                num_out_act_bound=-1):
+    """Implicit-GEMM tables (reference ``pairs.py:281-426``), the same 9-tuple."""
+    res, deferred = igemm_rulebook(indices, batch_size, spatial_shape, ksize, stride, padding,
+                                   dilation, out_padding, subm, transpose, is_train,
+                                   is_mask_split, do_sort, num_out_act_bound)
+    pm_fwd, pm_bwd, ma_fwd, ma_bwd = deferred.get()
+    return res[:4] + (pm_fwd, pm_bwd, ma_fwd, ma_bwd) + res[8:]
 
 
 def native_pair_to_tables(pair: torch.Tensor, indice_pair_num, n_in: int, n_out: int,

@@ -215,35 +215,33 @@ class SparseConvolutionBase:
                 self._require_inverse_source(datas)
                 outids = datas.indices
                 pair_fwd, pair_bwd = datas.pair_bwd, datas.pair_fwd
-                pm_fwd, pm_bwd = datas.pair_mask_bwd_splits, datas.pair_mask_fwd_splits
-                ma_fwd, ma_bwd = datas.mask_argsort_bwd_splits, datas.mask_argsort_fwd_splits
                 masks = datas.masks
                 out_spatial_shape = datas.spatial_shape
                 self._check_inverse_reuse_valid(x, spatial_shape, datas)
             elif datas is not None:
                 outids = datas.out_indices
                 pair_fwd, pair_bwd = datas.pair_fwd, datas.pair_bwd
-                pm_fwd, pm_bwd = datas.pair_mask_fwd_splits, datas.pair_mask_bwd_splits
-                ma_fwd, ma_bwd = datas.mask_argsort_fwd_splits, datas.mask_argsort_bwd_splits
                 masks = datas.masks
                 if not self.subm:
                     raise AssertionError("only support reuse subm indices")
                 self._check_subm_reuse_valid(x, spatial_shape, datas)
             else:
-                res = timed_pairgen(lambda: ops.get_indice_pairs_implicit_gemm(
+                # the mask sorts are deferred: the gather-GEMM does not read them
+                res, deferred = timed_pairgen(lambda: ops.implicit_gemm_rulebook(
                     x.indices, x.batch_size, spatial_shape, self.algo, ksize=self.kernel_size,
                     stride=self.stride, padding=self.padding, dilation=self.dilation,
                     out_padding=self.output_padding, subm=self.subm, transpose=self.transposed,
-                    is_train=(not self.subm) or training, alloc=x.thrust_allocator,
-                    timer=x._timer))
-                outids, pair_fwd, pair_bwd = res[0], res[2], res[3]
-                pm_fwd, pm_bwd, ma_fwd, ma_bwd, masks = res[4], res[5], res[6], res[7], res[8]
+                    is_train=(not self.subm) or training))
+                outids, pair_fwd, pair_bwd, masks = res[0], res[2], res[3], res[8]
                 if self.indice_key is not None:
                     register_implicit_gemm_indice_data(
                         indice_dict, self.indice_key, res, x.indices, is_subm=self.subm,
                         spatial_shape=spatial_shape, out_spatial_shape=out_spatial_shape,
                         algo=self.algo, ksize=self.kernel_size, stride=self.stride,
-                        dilation=self.dilation, padding=self.padding)
+                        dilation=self.dilation, padding=self.padding, deferred_masks=deferred)
+            # the kernels skip offsets without pairs themselves; the sorted
+            # mask splits would not change the result and are not passed
+            pm_fwd = pm_bwd = ma_fwd = ma_bwd = []
             if x.benchmark:
                 torch.cuda.synchronize()
                 bench_t = _time.time()

@@ -64,15 +64,17 @@ class ImplicitGemmIndiceData:
                  mask_argsort_bwd_splits: list[torch.Tensor], masks: list[np.ndarray],
                  spatial_shape, out_spatial_shape, is_subm: bool, algo: ConvAlgo,
                  ksize: list[int], stride: list[int], dilation: list[int], padding: list[int],
-                 in_voxel_num: Any | None = None, out_voxel_num: Any | None = None):
+                 in_voxel_num: Any | None = None, out_voxel_num: Any | None = None,
+                 deferred_masks: Any | None = None):
         self.out_indices = out_indices
         self.indices = indices
         self.pair_fwd = pair_fwd
         self.pair_bwd = pair_bwd
-        self.pair_mask_fwd_splits = pair_mask_fwd_splits
-        self.pair_mask_bwd_splits = pair_mask_bwd_splits
-        self.mask_argsort_fwd_splits = mask_argsort_fwd_splits
-        self.mask_argsort_bwd_splits = mask_argsort_bwd_splits
+        # the four mask-split lists; with deferred_masks (an object whose get()
+        # returns them) they are computed the first time one is read
+        self._mask_splits = [pair_mask_fwd_splits, pair_mask_bwd_splits,
+                             mask_argsort_fwd_splits, mask_argsort_bwd_splits]
+        self._deferred_masks = deferred_masks
         self.masks = masks
         self.spatial_shape = spatial_shape
         self.out_spatial_shape = out_spatial_shape
@@ -85,12 +87,31 @@ class ImplicitGemmIndiceData:
         self.in_voxel_num = in_voxel_num
         self.out_voxel_num = out_voxel_num
 
+    def _splits(self) -> list:
+        if self._deferred_masks is not None:
+            self._mask_splits = list(self._deferred_masks.get())
+            self._deferred_masks = None
+        return self._mask_splits
+
+    def _set_split(self, i: int, value) -> None:
+        self._splits()[i] = value
+
+    pair_mask_fwd_splits = property(lambda self: self._splits()[0],
+                                    lambda self, v: self._set_split(0, v))
+    pair_mask_bwd_splits = property(lambda self: self._splits()[1],
+                                    lambda self, v: self._set_split(1, v))
+    mask_argsort_fwd_splits = property(lambda self: self._splits()[2],
+                                       lambda self, v: self._set_split(2, v))
+    mask_argsort_bwd_splits = property(lambda self: self._splits()[3],
+                                       lambda self, v: self._set_split(3, v))
+
 
 def register_implicit_gemm_indice_data(indice_dict, indice_key, res, indices, *, is_subm,
                                        spatial_shape, out_spatial_shape, algo, ksize, stride,
-                                       dilation, padding):
+                                       dilation, padding, deferred_masks=None):
     """Store a ``get_indice_pairs_implicit_gemm`` 9-tuple under ``indice_key``;
-    an existing key is an error (reference core.py:123-164)."""
+    an existing key is an error (reference core.py:123-164).  ``deferred_masks``
+    (from ``ops.implicit_gemm_rulebook``) supplies the mask splits on first read."""
     if indice_key in indice_dict:
         raise AssertionError(f"your indice key {indice_key} already exists in this sparse tensor.")
     indice_dict[indice_key] = ImplicitGemmIndiceData(
@@ -98,7 +119,8 @@ def register_implicit_gemm_indice_data(indice_dict, indice_key, res, indices, *,
         pair_mask_fwd_splits=res[4], pair_mask_bwd_splits=res[5],
         mask_argsort_fwd_splits=res[6], mask_argsort_bwd_splits=res[7], masks=res[8],
         spatial_shape=spatial_shape, out_spatial_shape=out_spatial_shape, is_subm=is_subm,
-        algo=algo, ksize=ksize, stride=stride, dilation=dilation, padding=padding)
+        algo=algo, ksize=ksize, stride=stride, dilation=dilation, padding=padding,
+        deferred_masks=deferred_masks)
 
 
 def scatter_nd(indices: torch.Tensor, updates: torch.Tensor, shape):

@@ -101,6 +101,23 @@ def get_indice_pairs_implicit_gemm(indices: torch.Tensor, batch_size: int,
                               algo == ConvAlgo.MaskSplitImplicitGemm, do_sort, num_out_act_bound)
 
 
+def implicit_gemm_rulebook(indices: torch.Tensor, batch_size: int, spatial_shape: list[int],
+                           algo: ConvAlgo, ksize: list[int], stride: list[int],
+                           padding: list[int], dilation: list[int], out_padding: list[int],
+                           subm: bool = False, transpose: bool = False, is_train: bool = True,
+                           do_sort: bool = SPCONV_DO_SORT):
+    """``get_indice_pairs_implicit_gemm`` for the modules: the same 9-tuple with
+    empty mask-split lists, and a ``DeferredMaskSplits`` that computes them on
+    first use (the gather-GEMM does not read them)."""
+    if not indices.is_cuda:
+        raise AssertionError("implicit gemm only support gpu tensors")
+    if algo not in (ConvAlgo.MaskImplicitGemm, ConvAlgo.MaskSplitImplicitGemm):
+        raise AssertionError("TODO")
+    return _pairs.igemm_rulebook(indices, batch_size, spatial_shape, ksize, stride, padding,
+                                 dilation, out_padding, subm, transpose, is_train,
+                                 algo == ConvAlgo.MaskSplitImplicitGemm, do_sort)
+
+
 # ---------------------------------------------------------------------------
 # convolution
 # ---------------------------------------------------------------------------

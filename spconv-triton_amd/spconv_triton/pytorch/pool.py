@@ -62,18 +62,18 @@ class _PoolBase(SparseModule):
                                         self.padding, self.dilation)
 
     def _igemm_pairs(self, x: SparseConvTensor, indice_dict, out_spatial_shape):
-        res = ops.get_indice_pairs_implicit_gemm(
+        # pooling reads the gather tables only: the mask sorts are deferred
+        res, deferred = ops.implicit_gemm_rulebook(
             x.indices, x.batch_size, x.spatial_shape, self.algo, ksize=self.kernel_size,
             stride=self.stride, padding=self.padding, dilation=self.dilation,
             out_padding=[0] * self.ndim, subm=self.subm,
-            is_train=(not self.subm) or self.training, alloc=x.thrust_allocator,
-            timer=x._timer)
+            is_train=(not self.subm) or self.training)
         if self.indice_key is not None:
             register_implicit_gemm_indice_data(
                 indice_dict, self.indice_key, res, x.indices, is_subm=self.subm,
                 spatial_shape=x.spatial_shape, out_spatial_shape=out_spatial_shape,
                 algo=self.algo, ksize=self.kernel_size, stride=self.stride,
-                dilation=self.dilation, padding=self.padding)
+                dilation=self.dilation, padding=self.padding, deferred_masks=deferred)
         return res
 
     def _finish(self, out_tensor, outids, indice_dict, out_spatial_shape, out_features):

@@ -399,3 +399,64 @@ def test_mask_sort_stable_large(n, grid):
     np.testing.assert_array_equal(res[6][0].cpu().numpy(), exp)
     np.testing.assert_array_equal(res[4][0][:, 0].cpu().numpy().astype(np.int64) & 0xFFFFFFFF,
                                   words[exp])
+
+
+@pytest.mark.parametrize("training", [True, False])
+def test_module_rulebooks_defer_mask_sorts(training):
+    """Rulebooks built by the modules leave the mask sorts until a mask split is
+    read (the gather-GEMM never reads them).  Forward and backward must not
+    trigger them, and the values read afterwards, on the build stream or on
+    another stream, equal the oracle's bit for bit."""
+    import spconv_triton.pytorch as spconv
+
+    rng = np.random.default_rng(21)
+    shape = [24, 20, 18]
+    idx = rand_indices(rng, 2, shape, 1500)
+    t = torch.from_numpy(idx).to(DEV)
+    torch.manual_seed(0)
+    s1 = spconv.SubMConv3d(8, 8, 3, padding=1, indice_key="s1")
+    c2 = spconv.SparseConv3d(8, 8, 3, stride=2, padding=1, indice_key="c2")
+    s4 = spconv.SubMConv3d(8, 8, 3, padding=1, indice_key="s4")
+    p3 = spconv.SparseMaxPool3d(2, stride=2, indice_key="p3")
+    inv = spconv.SparseInverseConv3d(8, 8, 3, indice_key="c2")
+    for m in (s1, c2, s4, p3, inv):
+        m.to(DEV).train(training)
+    feats = torch.randn(idx.shape[0], 8, device=DEV, requires_grad=training)
+    h3 = s4(c2(s1(spconv.SparseConvTensor(feats, t, shape, 2))))
+    pooled = p3(h3)
+    y = inv(h3)
+    if training:
+        (y.features.square().sum() + pooled.features.sum()).backward()
+    torch.cuda.synchronize()
+    d = dict(y.indice_dict)
+    d["p3"] = pooled.indice_dict["p3"]
+    for key in ("s1", "c2", "s4", "p3"):
+        assert d[key]._deferred_masks is not None, f"{key}: masks were sorted by the module"
+
+    c2_out = d["c2"].out_indices.cpu().numpy()
+    c2_shape = list(d["c2"].out_spatial_shape)
+    cases = {  # key: (indices, geometry, is_train)
+        "s1": (idx, (shape, [3] * 3, [1] * 3, [1] * 3, [1] * 3, [0] * 3, True, False),
+               training),
+        "c2": (idx, (shape, [3] * 3, [2] * 3, [1] * 3, [1] * 3, [0] * 3, False, False), True),
+        "s4": (c2_out, (c2_shape, [3] * 3, [1] * 3, [1] * 3, [1] * 3, [0] * 3, True, False),
+               training),
+        "p3": (c2_out, (c2_shape, [2] * 3, [2] * 3, [0] * 3, [1] * 3, [0] * 3, False, False),
+               True),
+    }
+    side = torch.cuda.Stream()
+    for j, (key, (ind, g, is_train)) in enumerate(cases.items()):
+        data = d[key]
+        if j % 2:  # first read on another stream
+            with torch.cuda.stream(side):
+                splits = (data.pair_mask_fwd_splits, data.pair_mask_bwd_splits,
+                          data.mask_argsort_fwd_splits, data.mask_argsort_bwd_splits)
+            torch.cuda.current_stream().wait_stream(side)
+        else:
+            splits = (data.pair_mask_fwd_splits, data.pair_mask_bwd_splits,
+                      data.mask_argsort_fwd_splits, data.mask_argsort_bwd_splits)
+        assert data._deferred_masks is None
+        shape_k, ks, st, pad, dil, op, subm, tr = g
+        exp = orc.igemm_pairs(ind, 2, shape_k, ks, st, pad, dil, op, subm, tr, is_train)
+        res = (data.out_indices, exp[1], data.pair_fwd, data.pair_bwd) + splits + (data.masks,)
+        _compare_igemm(res, exp, data.indices if subm else None, subm, is_train)
