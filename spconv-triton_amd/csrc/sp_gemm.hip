@@ -145,17 +145,30 @@ __device__ __forceinline__ typename Mfma<T>::frag load_frag_vec(const T* p) {
 // dW[n, k, c] = sum over the pairs (i, o) of offset k of X[i, c] * G[o, n]:
 // per offset a GEMM whose reduction runs over that offset's compacted pair
 // list.  A workgroup owns (offset k, a contiguous share of its pairs, a
-// 64 x 64 block of (c, n)); each wave a 32 x 32 block.  The MFMA operands
-// need the pair index as the reduction index, i.e. X and G transposed, so the
-// rows gathered for a stage of kWgStage pairs are written to LDS as
-// [channel][pair] (two pairs per 32-bit write) and read back as 16-byte
-// fragments.  Gathers are 16-byte vector loads; the next stage's rows and the
-// pair indices two stages ahead are in flight while the stage's MFMAs run.
+// BW x BW block of (c, n)); each wave a BW/2 x BW/2 block of 32x32 MFMA tiles.
+// The MFMA operands need the pair index as the reduction index, i.e. X and G
+// transposed, so the rows gathered for a stage of pairs are written to LDS as
+// [channel][pair] (two pairs per write) and read back as 16-byte fragments.
+// Gathers are 16-byte vector loads; the next stage's rows and the pair indices
+// two stages ahead are in flight while the stage's MFMAs run.  Every (c, n)
+// block gathers the rows of all its pairs again, so wide layers take
+// BW = 128: half the gathered bytes of BW = 64 at C, K >= 128.
 // fp32 partials per share are summed in a fixed order by wgrad_reduce
 // (deterministic, no atomics).
-constexpr int kWgStage = 128;  // pairs per LDS stage
+template <typename T, int BW>
+struct WgShape {
+  static constexpr int kStage = BW == 64 || sizeof(T) == 2 ? 128 : 64;  // pairs per LDS stage
+  static constexpr int kPitch = kStage + Mfma<T>::V;   // LDS row pitch (rows stay 16-B aligned)
+  static constexpr int kPairRows = kStage / 2;         // staging threads per channel group
+  static constexpr int kGroups = 256 / kPairRows;      // channel groups of the staging threads
+  static constexpr int kCh = BW / kGroups;             // channels per staging thread
+  static constexpr int kNv = kCh / Mfma<T>::V;         // vectors per thread, tensor and pair
+  static constexpr int kMt = BW / 64;                  // 32x32 tiles per wave and dimension
+  static_assert(kCh % Mfma<T>::V == 0 && kStage % Mfma<T>::KSTEP == 0, "wgrad staging shape");
+  static_assert(2 * BW * kPitch * sizeof(T) <= 72 * 1024, "wgrad LDS");
+};
 
-template <typename T, bool VEC>
+template <typename T, bool VEC, int BW>
 __global__ __launch_bounds__(256) void wgrad_partial(
     const T* __restrict__ X, int64_t n_in, const T* __restrict__ G, int64_t n_out, int C, int K,
     int kv, const int32_t* __restrict__ in_rows, const int32_t* __restrict__ out_rows,
@@ -163,23 +176,23 @@ __global__ __launch_bounds__(256) void wgrad_partial(
     uint32_t x_bytes, uint32_t g_bytes) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
+  using S = WgShape<T, BW>;
   constexpr int V = MF::V;
   constexpr int KSTEP = MF::KSTEP;
   constexpr uint32_t ES = sizeof(T);
-  constexpr int PITCH = kWgStage + V;  // row pitch in elements (rows stay 16-byte aligned)
-  constexpr int NV = 16 / V;           // vectors per thread, tensor and pair (16 channels)
-  __shared__ __align__(16) T Xs[64][PITCH];
-  __shared__ __align__(16) T Gs[64][PITCH];
+  constexpr int STAGE = S::kStage, PITCH = S::kPitch, NV = S::kNv, MT = S::kMt;
+  __shared__ __align__(16) T Xs[BW][PITCH];
+  __shared__ __align__(16) T Gs[BW][PITCH];
 
   const int k = blockIdx.x / splits;
   const int split = blockIdx.x % splits;
-  const int c0 = blockIdx.y * 64, n0 = blockIdx.z * 64;
+  const int c0 = blockIdx.y * BW, n0 = blockIdx.z * BW;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int h = lane >> 5, l32 = lane & 31;
-  const int ctile = (wave >> 1) * 32, ntile = (wave & 1) * 32;
-  // staging role: pairs 2 pp and 2 pp + 1 of a stage, channels 16 q .. 16 q + 15
-  const int pp = tid & 63, q = tid >> 6;
+  const int ctile = (wave >> 1) * (BW / 2), ntile = (wave & 1) * (BW / 2);
+  // staging role: pairs 2 pp and 2 pp + 1 of a stage, channels kCh q .. kCh q + kCh - 1
+  const int pp = tid % S::kPairRows, q = tid / S::kPairRows;
 
   const int64_t cnt = counts[k];
   const int64_t chunk = (cnt + splits - 1) / splits;
@@ -212,7 +225,7 @@ __global__ __launch_bounds__(256) void wgrad_partial(
     for (int e = 0; e < 2; ++e)
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
-        const int cx = c0 + q * 16 + j * V, nx = n0 + q * 16 + j * V;
+        const int cx = c0 + q * S::kCh + j * V, nx = n0 + q * S::kCh + j * V;
         if (VEC) {
           xv[e][j] = buf_frag<T>(rx, row_off(iv[e], cx, C, C));
           gv[e][j] = buf_frag<T>(rg, row_off(ov[e], nx, K, K));
@@ -231,7 +244,7 @@ __global__ __launch_bounds__(256) void wgrad_partial(
     for (int j = 0; j < NV; ++j)
 #pragma unroll
       for (int t = 0; t < V; ++t) {
-        const int c = q * 16 + j * V + t;
+        const int c = q * S::kCh + j * V + t;
         const T2 xp = {xv[0][j][t], xv[1][j][t]};
         const T2 gp = {gv[0][j][t], gv[1][j][t]};
         *reinterpret_cast<T2*>(&Xs[c][2 * pp]) = xp;
@@ -239,16 +252,20 @@ __global__ __launch_bounds__(256) void wgrad_partial(
       }
   };
 
-  floatx16 acc;
+  floatx16 acc[MT][MT];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  for (int a = 0; a < MT; ++a)
+#pragma unroll
+    for (int b = 0; b < MT; ++b)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.f;
 
   int32_t iv[2], ov[2], iv2[2], ov2[2];
   frag xv[2][NV], gv[2][NV];
   load_idx(p_lo, iv, ov);
   load_rows(iv, ov, xv, gv);
-  load_idx(p_lo + kWgStage, iv2, ov2);
-  for (int64_t s0 = p_lo; s0 < p_hi; s0 += kWgStage) {
+  load_idx(p_lo + STAGE, iv2, ov2);
+  for (int64_t s0 = p_lo; s0 < p_hi; s0 += STAGE) {
     __syncthreads();  // the previous stage's fragments are read
     put_rows(xv, gv);
     __syncthreads();
@@ -259,21 +276,33 @@ __global__ __launch_bounds__(256) void wgrad_partial(
       ov[e] = ov2[e];
     }
     load_rows(iv, ov, xv, gv);
-    load_idx(s0 + 2 * kWgStage, iv2, ov2);
+    load_idx(s0 + 2 * STAGE, iv2, ov2);
 #pragma unroll
-    for (int st = 0; st < kWgStage; st += KSTEP) {
-      const frag a = *reinterpret_cast<const frag*>(&Xs[ctile + l32][st + h * V]);
-      const frag b = *reinterpret_cast<const frag*>(&Gs[ntile + l32][st + h * V]);
-      MF::mma(a, b, acc);
+    for (int st = 0; st < STAGE; st += KSTEP) {
+      frag a[MT], b[MT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        a[m] = *reinterpret_cast<const frag*>(&Xs[ctile + 32 * m + l32][st + h * V]);
+        b[m] = *reinterpret_cast<const frag*>(&Gs[ntile + 32 * m + l32][st + h * V]);
+      }
+#pragma unroll
+      for (int mc = 0; mc < MT; ++mc)
+#pragma unroll
+        for (int mn = 0; mn < MT; ++mn) MF::mma(a[mc], b[mn], acc[mc][mn]);
     }
   }
   // D[c][n]: lane holds column n = l32 of rows c = 8*(i/4) + 4*h + (i%4)
-  const int n = n0 + ntile + l32;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int c = c0 + ctile + (i >> 2) * 8 + h * 4 + (i & 3);
-    if (c < C && n < K) part[((int64_t(split) * K + n) * kv + k) * C + c] = acc[i];
-  }
+  for (int mc = 0; mc < MT; ++mc)
+#pragma unroll
+    for (int mn = 0; mn < MT; ++mn) {
+      const int n = n0 + ntile + 32 * mn + l32;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int c = c0 + ctile + 32 * mc + (i >> 2) * 8 + h * 4 + (i & 3);
+        if (c < C && n < K) part[((int64_t(split) * K + n) * kv + k) * C + c] = acc[mc][mn][i];
+      }
+    }
 }
 
 template <typename T>
@@ -527,8 +556,12 @@ static int gemm_common(const void* A, int dtype, int64_t n_src, const void* w, i
                      nullptr, 0, out, out_dtype, s);
 }
 
+// (c, n) block width of the weight-gradient workgroups
+static int wgrad_block(int64_t C, int64_t K) { return C >= 128 && K >= 128 ? 128 : 64; }
+
 static int wgrad_splits(int64_t kv, int64_t C, int64_t K, int64_t n_rows) {
-  const int64_t tiles = kv * cdiv(C, 64) * cdiv(K, 64);
+  const int bw = wgrad_block(C, K);
+  const int64_t tiles = kv * cdiv(C, bw) * cdiv(K, bw);
   int64_t splits = cdiv(1024, tiles);           // aim for ~4 workgroups per CU on 256 CUs
   const int64_t by_len = cdiv(n_rows, 1024);    // keep >= ~1k rows of work per split
   if (splits > by_len) splits = by_len;
@@ -622,12 +655,14 @@ int sp_conv_wgrad(const void* x, int64_t n_in, const void* g, int64_t n_out, int
   const int v = vec_of(dtype);
   const bool vec = C % v == 0 && K % v == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(g) % 16 == 0;
-  dim3 grid(unsigned(gx), unsigned(cdiv(C, 64)), unsigned(cdiv(K, 64)));
+  const int bw = wgrad_block(C, K);
+  dim3 grid(unsigned(gx), unsigned(cdiv(C, bw)), unsigned(cdiv(K, bw)));
   const int64_t tot = K * kv * C;
   const unsigned rb = unsigned(cdiv(tot, 256));
   auto run = [&](auto tag) {
     using T = decltype(tag);
-    auto kern = vec ? wgrad_partial<T, true> : wgrad_partial<T, false>;
+    auto kern = bw == 128 ? (vec ? wgrad_partial<T, true, 128> : wgrad_partial<T, false, 128>)
+                          : (vec ? wgrad_partial<T, true, 64> : wgrad_partial<T, false, 64>);
     kern<<<grid, 256, 0, s>>>(static_cast<const T*>(x), n_in, static_cast<const T*>(g), n_out,
                               int(C), int(K), int(kv), in_rows, out_rows, counts, row_stride,
                               splits, part, uint32_t(xb), uint32_t(gb));

@@ -74,6 +74,10 @@ CASES = [
     (6, 16, 2500, False, 2),
     (128, 96, 3000, True, 1),
     (40, 24, 2500, True, 1),
+    # wide layers: the weight gradient takes 128 x 128 (c, n) blocks
+    (128, 256, 2500, True, 1),
+    (256, 136, 3000, False, 2),
+    (130, 128, 2000, True, 1),  # rows not a whole number of 16-byte vectors
 ]
 
 
@@ -118,7 +122,7 @@ def test_forward_output_dtype(out_dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("ci", [0, 1, 3, 5, 6])
+@pytest.mark.parametrize("ci", [0, 1, 3, 5, 6, 8, 9, 10])
 def test_dgrad_and_wgrad_match_oracle(ci, dtype):
     from spconv_triton.pytorch._impl import gemm
 
