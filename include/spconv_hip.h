@@ -198,6 +198,38 @@ int sp_conv_gemm_planned(const void* a, int32_t dtype, int64_t n_src, const void
                          const int32_t* pairs, int64_t M, const void* plan, size_t plan_bytes,
                          void* out, int32_t out_dtype, void* stream);
 
+/* The gather-GEMM with the output rows taken in a given order: tile row i is
+ * output row row_order[i] (a permutation of 0..M-1, here the stable mask
+ * argsort), pairs_perm is the table permuted by it (sp_permute_table) and
+ * plan (nullable, kv <= 64) a gather plan of pairs_perm.  Results are
+ * bit-identical to the natural order's.  This is the reference's masked
+ * traversal, which visits rows in mask_argsort order so that a row tile holds
+ * rows with similar masks (gemm.py:282-296, the mask_argsort operand of
+ * _gather_gemm_kernel :501-568); with the table permuted up front the kernel
+ * reads it coalesced. */
+int sp_conv_gemm_ordered(const void* a, int32_t dtype, int64_t n_src, const void* packed,
+                         int64_t K, int64_t kv, int64_t C, int32_t transpose, int32_t has_bias,
+                         const int32_t* pairs_perm, int64_t M, const int32_t* row_order,
+                         const void* plan, size_t plan_bytes, void* out, int32_t out_dtype,
+                         void* stream);
+
+/* out[k, i] = pairs[k, order[i]] for a gather table pairs [kv, M] (-1 where
+ * order[i] is outside 0..M-1).  Builds the pairs_perm of sp_conv_gemm_ordered
+ * (the reference indexes the table through mask_argsort inside its kernel,
+ * gemm.py:501-568). */
+int sp_permute_table(const int32_t* pairs, int64_t kv, int64_t M, const int32_t* order,
+                     int32_t* out, void* stream);
+
+/* Work statistics of a gather table [kv, M] in its own row order, added into
+ * stats[0..2] (int64, zeroed by the caller): the pairs (entries in
+ * 0..n_src-1), the (256-row tile, offset) pairs with at least one pair and
+ * the (64-row block, offset) pairs with at least one pair.  pairs / (256 *
+ * stats[1]) is the share of the staged GEMM's MFMA work spent on pairs, which
+ * decides whether a table is worth reordering.  No reference counterpart: the
+ * reference always takes the mask-sorted order (gemm.py:282-296). */
+int sp_table_stats(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_src, int64_t* stats,
+                   void* stream);
+
 /* Forward: out[m, n] = bias[n] + sum_k sum_c X[pf[k, m], c] * W[n, k, c].
  * X [n_in, C] dtype; W [K, kv, C] w_dtype; pf [kv, n_out]; bias [K] of
  * w_dtype (nullable); out [n_out, K] out_dtype.  pair_mask/mask_argsort [n_out]

@@ -16,9 +16,15 @@
 //
 // Masked mode (MaskImplicitGemm, gemm.py:282-296): the reference visits rows in
 // mask_argsort order to skip offsets that are empty for a whole tile.  Here the
-// kernel skips such offsets per 64-row wave tile by itself (a ballot over the
-// rows' pairs) and keeps the rows' natural order; skipped terms are exactly
-// zero, so the result equals the dense one.
+// kernels skip such offsets per tile (staged) or 64-row wave tile (direct) by
+// themselves and by default keep the rows' natural order, whose tiles share
+// most of their source rows.  For sparse tables, whose natural tiles have a
+// pair for most offsets but in few rows, the ordered entry point takes the
+// rows in a given order (the stable mask argsort): the table is permuted once
+// (sp_permute_table), tile row i is output row order[i], and rows with equal
+// masks share tiles, so far fewer offsets are live per tile.  Skipped terms
+// are exactly zero and every row sums its offsets in ascending order, so all
+// orders give the same result bit for bit.
 //
 // Weight gradient (gemm.py:324-426): per offset k, dW[k] = X_k^T G_k over the
 // compacted pairs of that offset.  The pair dimension is the MFMA reduction
@@ -390,6 +396,7 @@ struct GemmCall {
   bool planned;
   PlanDev plan;
   const float* bias;
+  const int32_t* order;  // tile row -> output row, or null (natural order)
   bool vec;
 };
 
@@ -412,7 +419,8 @@ static int launch_direct(dim3 grid, hipStream_t s, const T* A, const T* bt, cons
   int rc = allow_lds(reinterpret_cast<const void*>(kern),
                      direct_lds(kGroupOffsets + kPad, uint32_t(sizeof(OutT))).total, attr_set);
   if (rc) return rc;
-  kern<<<grid, 256, lds, s>>>(A, bt, pairs, c.bias, o, nb, c.n_src, c.M, c.N, c.R, c.Rp, c.kv);
+  kern<<<grid, 256, lds, s>>>(A, bt, pairs, c.order, c.bias, o, nb, c.n_src, c.M, c.N, c.R, c.Rp,
+                              c.kv);
   SP_LAUNCHED();
   return SP_OK;
 }
@@ -435,8 +443,8 @@ static int launch_staged(dim3 grid, hipStream_t s, const T* A, const T* bt, cons
   int rc = allow_lds(reinterpret_cast<const void*>(kern),
                      staged_kernel_lds(kPlanMaxKv, kPlanMaxKv, uint32_t(sizeof(OutT))), attr_set);
   if (rc) return rc;
-  kern<<<grid, 256, lds, s>>>(A, bt, pairs, c.plan, c.bias, o, nb, c.n_src, c.M, c.N, c.R, c.Rp,
-                              c.kv);
+  kern<<<grid, 256, lds, s>>>(A, bt, pairs, c.order, c.plan, c.bias, o, nb, c.n_src, c.M, c.N,
+                              c.R, c.Rp, c.kv);
   SP_LAUNCHED();
   return SP_OK;
 }
@@ -494,11 +502,14 @@ static int launch_gemm_out(int out_dtype, const T* A, const T* bt, const int32_t
   }
 }
 
-// plan (nullable) is a gather plan of `pairs` built by sp_gather_plan_build.
+// plan (nullable) is a gather plan of `pairs` built by sp_gather_plan_build;
+// order (nullable) maps tile rows to output rows (`pairs` is then the table
+// permuted by it).
 static int gemm_packed(const void* A, int dtype, int64_t n_src, const void* packed, int64_t K,
                        int64_t kv, int64_t C, int transpose, int has_bias, const int32_t* pairs,
                        int64_t M, const int32_t* pm, const int32_t* ar, const void* plan,
-                       size_t plan_bytes, void* out, int out_dtype, hipStream_t s) {
+                       size_t plan_bytes, void* out, int out_dtype, hipStream_t s,
+                       const int32_t* order = nullptr) {
   SP_CHECK_ARG(gemm_dtype_ok(dtype), "gemm: feature dtype %d not supported (f16/bf16/f32)", dtype);
   SP_CHECK_ARG(K >= 1 && C >= 1 && kv >= 1 && M >= 0 && n_src >= 0, "gemm: bad sizes");
   SP_CHECK_ARG(K < 65536 && C < 65536 && kv < 65536, "gemm: channel/kernel size too large");
@@ -516,6 +527,7 @@ static int gemm_packed(const void* A, int dtype, int64_t n_src, const void* pack
   c.Rp = p.Rp;
   c.kv = int(kv);
   c.bias = has_bias ? reinterpret_cast<const float*>(base + p.bias_off) : nullptr;
+  c.order = order;
   c.vec = (p.R % vec_of(dtype) == 0) && (reinterpret_cast<uintptr_t>(A) % 16 == 0);
   c.planned = plan != nullptr;
   c.plan = PlanDev{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0};
@@ -607,6 +619,17 @@ int sp_conv_gemm_planned(const void* a, int32_t dtype, int64_t n_src, const void
   SP_CHECK_ARG(plan != nullptr, "gemm: null gather plan");
   return gemm_packed(a, dtype, n_src, packed, K, kv, C, transpose, has_bias, pairs, M, nullptr,
                      nullptr, plan, plan_bytes, out, out_dtype, as_stream(stream));
+}
+
+int sp_conv_gemm_ordered(const void* a, int32_t dtype, int64_t n_src, const void* packed,
+                         int64_t K, int64_t kv, int64_t C, int32_t transpose, int32_t has_bias,
+                         const int32_t* pairs_perm, int64_t M, const int32_t* row_order,
+                         const void* plan, size_t plan_bytes, void* out, int32_t out_dtype,
+                         void* stream) {
+  SP_CHECK_ARG(row_order != nullptr, "gemm: null row order");
+  return gemm_packed(a, dtype, n_src, packed, K, kv, C, transpose, has_bias, pairs_perm, M,
+                     nullptr, nullptr, plan, plan_bytes, out, out_dtype, as_stream(stream),
+                     row_order);
 }
 
 int sp_conv_fwd(const void* x, int32_t dtype, int64_t n_in, int64_t C, const void* w,

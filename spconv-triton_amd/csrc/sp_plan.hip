@@ -250,6 +250,50 @@ __global__ __launch_bounds__(256) void plan_overflow_kernel(const int32_t* __res
   if (threadIdx.x == 0) *n_overflow = int32_t(base);
 }
 
+// Per 256-row tile of a gather table: its pairs (valid entries), the offsets
+// with a pair in the tile and the (64-row wave block, offset) pairs with a
+// pair, summed into stats[0..2] (zeroed by the caller).  Measured in a given
+// row order, they give the share of a GEMM's MFMA work spent on pairs: the
+// staged kernel runs 256 rows per live tile offset, the direct one 64 rows
+// per live wave offset.
+__global__ __launch_bounds__(256) void table_stats_kernel(const int32_t* __restrict__ pairs,
+                                                          int64_t M, int kv, int64_t n_src,
+                                                          unsigned long long* __restrict__ stats) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int64_t r = int64_t(blockIdx.x) * 256 + tid;
+  uint32_t npair = 0, wave_live = 0, tile_live = 0;
+  for (int k = 0; k < kv; ++k) {
+    bool ok = false;
+    if (r < M) {
+      const int32_t x = pairs[int64_t(k) * M + r];
+      ok = x >= 0 && x < n_src;
+    }
+    npair += ok ? 1u : 0u;
+    wave_live += __builtin_amdgcn_ballot_w64(ok) != 0 ? 1u : 0u;
+    tile_live += __syncthreads_or(ok) ? 1u : 0u;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) npair += __shfl_xor(npair, off, 64);
+  if (lane == 0) {
+    atomicAdd(&stats[0], (unsigned long long)npair);
+    atomicAdd(&stats[2], (unsigned long long)wave_live);
+    if (tid == 0) atomicAdd(&stats[1], (unsigned long long)tile_live);
+  }
+}
+
+// out[k, i] = pairs[k, order[i]]: the table in a given row order (-1 where
+// order[i] is not a row).
+__global__ __launch_bounds__(256) void permute_table_kernel(const int32_t* __restrict__ pairs,
+                                                            int64_t M, int kv,
+                                                            const int32_t* __restrict__ order,
+                                                            int32_t* __restrict__ out) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= M) return;
+  const int32_t src = order[i];
+  const bool ok = src >= 0 && src < M;
+  for (int k = 0; k < kv; ++k) out[int64_t(k) * M + i] = ok ? pairs[int64_t(k) * M + src] : -1;
+}
+
 template <int NP>
 static void launch_plan(unsigned nt, hipStream_t s, const int32_t* pairs, int64_t M, int kv,
                         int64_t n_src, const PlanLayout& p, char* b) {
@@ -306,6 +350,32 @@ int sp_gather_plan_build(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_
     SP_HIP(hipStreamSynchronize(s));
     *n_overflow = h;
   }
+  return SP_OK;
+}
+
+int sp_table_stats(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_src, int64_t* stats,
+                   void* stream) {
+  SP_CHECK_ARG(kv >= 1 && M >= 0 && n_src >= 0, "table stats: bad sizes");
+  if (M == 0) return SP_OK;
+  SP_CHECK_ARG(pairs && stats, "table stats: null pointer");
+  const int64_t nt = cdiv(M, int64_t(256));
+  SP_CHECK_ARG(nt <= kMaxGridX && kv < 65536, "table stats: too many rows");
+  table_stats_kernel<<<unsigned(nt), 256, 0, as_stream(stream)>>>(
+      pairs, M, int(kv), n_src, reinterpret_cast<unsigned long long*>(stats));
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+int sp_permute_table(const int32_t* pairs, int64_t kv, int64_t M, const int32_t* order,
+                     int32_t* out, void* stream) {
+  SP_CHECK_ARG(kv >= 1 && M >= 0, "permute table: bad sizes");
+  if (M == 0) return SP_OK;
+  SP_CHECK_ARG(pairs && order && out, "permute table: null pointer");
+  const int64_t nb = cdiv(M, int64_t(256));
+  SP_CHECK_ARG(nb <= kMaxGridX && kv < 65536, "permute table: too many rows");
+  permute_table_kernel<<<unsigned(nb), 256, 0, as_stream(stream)>>>(pairs, M, int(kv), order,
+                                                                     out);
+  SP_LAUNCHED();
   return SP_OK;
 }
 

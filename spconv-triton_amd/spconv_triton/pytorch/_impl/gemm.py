@@ -16,6 +16,7 @@ least as accurate.  The flags are still accepted.
 from __future__ import annotations
 
 import ctypes
+import os
 import weakref
 
 import torch
@@ -118,6 +119,91 @@ def gather_plan(pairs: torch.Tensor, n_src: int):
     return plan
 
 
+#: Row order of the forward / input-gradient GEMMs.  "natural": the table's
+#: own order, whose 256-row tiles share most of their source rows (staged once
+#: per tile in LDS).  "mask": the stable argsort of the rows' masks, the
+#: reference's order (gemm.py:282-296), whose tiles hold rows with similar
+#: masks and so have fewer live offsets, but more distinct source rows (tiles
+#: whose rows do not fit in LDS are gathered directly).  "auto": natural,
+#: unless the layer is wide (C * K >= ORDER_MIN_WORK), the natural tiles spend
+#: less than ORDER_MAX_EFFICIENCY of their MFMA work on pairs, and the mask
+#: order cuts that work to at most ORDER_MAX_WORK_RATIO of it.  The checks read
+#: counters back once per table (one or two stream synchronizations).  Every
+#: order gives bit-identical results.
+ROW_ORDER = os.environ.get("SPCONV_GEMM_ROW_ORDER", "auto")
+ORDER_MIN_WORK = 128 * 128
+ORDER_MAX_EFFICIENCY = 0.2
+ORDER_MAX_WORK_RATIO = 0.35
+_PLAN_MAX_KV = 64  # kv range of the gather plans (sp_gather_plan_bytes)
+
+
+def table_stats(pairs: torch.Tensor, n_src: int) -> tuple[int, int, int]:
+    """(pairs, live (256-row tile, offset) pairs, live (64-row block, offset)
+    pairs) of a [kv, M] table in its own row order (``sp_table_stats``).
+    Reading them synchronizes."""
+    kv, M = pairs.shape
+    stats = torch.zeros(3, dtype=torch.int64, device=pairs.device)
+    _lib.check(_lib.lib().sp_table_stats(_lib.ptr(pairs), kv, M, int(n_src), _lib.ptr(stats),
+                                         _lib.stream_of(pairs.device)), "sp_table_stats")
+    return tuple(int(v) for v in stats.cpu())
+
+
+def mask_order(pairs: torch.Tensor) -> torch.Tensor:
+    """Stable argsort of the rows' masks of a [kv, M] table, as the reference's
+    mask_argsort (pairs.py:356-392) orders them: int32 [M]."""
+    from . import pairs as _pairs
+    kv = pairs.shape[0]
+    words = _pairs.mask_words(pairs)
+    _, ar = _pairs.sort_mask_words(words, kv, _pairs.split_masks(kv, False), True)
+    return ar[0]
+
+
+def permute_table(pairs: torch.Tensor, order: torch.Tensor) -> torch.Tensor:
+    """out[k, i] = pairs[k, order[i]] (``sp_permute_table``)."""
+    kv, M = pairs.shape
+    out = torch.empty_like(pairs)
+    _lib.check(_lib.lib().sp_permute_table(_lib.ptr(pairs), kv, M, _lib.ptr(order), _lib.ptr(out),
+                                           _lib.stream_of(pairs.device)), "sp_permute_table")
+    return out
+
+
+def row_order_variant(pairs: torch.Tensor, n_src: int, work: int):
+    """(order, permuted table, its gather plan or None) when a GEMM of
+    ``work`` = C * K on this table should take its rows in mask order (see
+    ROW_ORDER), else None.  Memoised on the table tensor like its plan."""
+    mode = ROW_ORDER
+    if mode == "natural":
+        return None
+    if mode not in ("auto", "mask"):
+        raise ValueError(f"SPCONV_GEMM_ROW_ORDER must be auto, natural or mask, not {mode!r}")
+    stamp = (int(n_src), pairs._version, pairs.data_ptr(), mode)
+    cached = getattr(pairs, "_spconv_triton_order", None)
+    if cached is not None and cached[0] == stamp:
+        return cached[1]
+    kv, M = pairs.shape
+
+    def mfma_rows(stats):  # rows the GEMM multiplies: per live tile or wave offset
+        return 256 * stats[1] if kv <= _PLAN_MAX_KV else 64 * stats[2]
+
+    if mode == "auto":
+        if work < ORDER_MIN_WORK or M == 0:
+            return None  # not decided: a wider layer on this table may still reorder
+        natural = table_stats(pairs, n_src)
+        done = mfma_rows(natural)
+        if done == 0 or natural[0] >= ORDER_MAX_EFFICIENCY * done:
+            pairs._spconv_triton_order = (stamp, None)
+            return None
+    order = mask_order(pairs)
+    perm = permute_table(pairs, order)
+    if mode == "auto" and mfma_rows(table_stats(perm, n_src)) > ORDER_MAX_WORK_RATIO * done:
+        pairs._spconv_triton_order = (stamp, None)
+        return None
+    plan = gather_plan(perm, n_src) if USE_GATHER_PLAN else None
+    variant = (order, perm, plan)
+    pairs._spconv_triton_order = (stamp, variant)
+    return variant
+
+
 def plan_overflow_count(plan: torch.Tensor) -> int:
     """Number of tiles of a plan whose distinct rows do not fit in LDS (the
     plan's first int32; reading it synchronizes)."""
@@ -130,6 +216,15 @@ def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: 
     kv = pairs.shape[0]
     packed = packed_weight(filters, bias, a.dtype, transpose)
     L = _lib.lib()
+    variant = row_order_variant(pairs, a.shape[0], K * C)
+    if variant is not None:
+        order, perm, plan = variant
+        _lib.check(L.sp_conv_gemm_ordered(
+            _lib.ptr(a), _lib.dtype_code(a.dtype), a.shape[0], _lib.ptr(packed), K, kv, C,
+            int(transpose), int(bias is not None), _lib.ptr(perm), M, _lib.ptr(order),
+            _lib.ptr(plan), 0 if plan is None else plan.numel(), _lib.ptr(out),
+            _lib.dtype_code(out.dtype), _lib.stream_of(a.device)), "sp_conv_gemm_ordered")
+        return
     plan = gather_plan(pairs, a.shape[0]) if USE_GATHER_PLAN else None
     if plan is not None:
         # the planned kernel skips empty offsets itself: mask tables are not needed

@@ -225,3 +225,118 @@ def test_planned_metric_shape():
     b = torch.randn(64, device=DEV).half()
     planned, direct = _both(x, w, b, False, pf, pf.shape[1])
     assert torch.equal(planned, direct)
+
+
+# ---------------------------------------------------------------------------
+# row order: the GEMM over the rows in mask-argsort order
+# ---------------------------------------------------------------------------
+
+def test_table_stats_and_permute():
+    """sp_table_stats counts pairs (sources in range only) and live (tile,
+    offset) / (64-row block, offset) pairs; sp_permute_table gathers columns."""
+    from spconv_triton.pytorch._impl import gemm
+
+    rng = np.random.default_rng(31)
+    for kv, M, n_src, p in [(27, 1000, 5000, 0.2), (125, 700, 300, 0.03), (8, 1, 10, 1.0),
+                            (27, 512, 900, 0.0)]:
+        t = _random_table(rng, kv, M, n_src, p)
+        if M > 10:
+            t[3, 5:9] = n_src + 2  # out of range: not a pair
+        tn = t.cpu().numpy()
+        ok = (tn >= 0) & (tn < n_src)
+        got = gemm.table_stats(t, n_src)
+        pad = lambda b: np.pad(ok, ((0, 0), (0, -M % b))).reshape(kv, -1, b).any(axis=2).sum()
+        assert got == (int(ok.sum()), int(pad(256)), int(pad(64))), (kv, M, got)
+        order_np = rng.permutation(M).astype(np.int32)
+        perm = gemm.permute_table(t, torch.from_numpy(order_np).to(DEV))
+        np.testing.assert_array_equal(perm.cpu().numpy(), tn[:, order_np])
+
+
+def _orders(a, w, bias, transpose, pairs, M):
+    """The GEMM in natural and in mask row order, planned and unplanned."""
+    from spconv_triton.pytorch._impl import gemm
+
+    N = w.shape[-1] if transpose else w.shape[0]
+    outs = {}
+    for mode in ("natural", "mask"):
+        for use in (True, False):
+            gemm.ROW_ORDER, gemm.USE_GATHER_PLAN = mode, use
+            try:
+                out = torch.empty((M, N), dtype=a.dtype, device=DEV)
+                gemm._gemm(a, w, bias, transpose, pairs, M, None, None, out)
+                outs[(mode, use)] = out
+            finally:
+                gemm.ROW_ORDER, gemm.USE_GATHER_PLAN = "auto", True
+    return outs
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("case", ["subm", "strided", "kv125", "sparse_wide"])
+def test_mask_row_order_bit_identical(case, dtype):
+    """Every row sums its offsets in ascending order whatever tile it falls in,
+    so the mask-ordered GEMM (staged, overflow and direct tiles) equals the
+    natural-order one bit for bit, forward and input gradient."""
+    from spconv_triton.pytorch._impl import gemm
+
+    rng = np.random.default_rng(44)
+    ks, C, K = 3, 32, 48
+    if case == "subm":
+        grid, n, stride = 28, 6000, 1
+    elif case == "strided":
+        grid, n, stride = 28, 5000, 2
+    elif case == "kv125":
+        grid, n, stride, ks = 20, 2500, 1, 5
+    else:  # wide layer; in mask order 18 of the 47 tiles overflow LDS
+        grid, n, stride, C, K = 40, 6000, 1, 136, 128
+    idx = rand_indices(rng, 2, [grid] * 3, n)
+    subm = stride == 1
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+    res = ops.get_indice_pairs_implicit_gemm(torch.from_numpy(idx).to(DEV), 2, [grid] * 3,
+                                             ConvAlgo.MaskImplicitGemm, [ks] * 3, [stride] * 3,
+                                             [ks // 2] * 3, [1] * 3, [0] * 3, subm, False,
+                                             is_train=True)
+    pf, pb = res[2], res[3]
+    kv = ks ** 3
+    torch.manual_seed(3)
+    x, _ = _q(torch.randn(idx.shape[0], C), dtype)
+    w, _ = _q(torch.randn(K, kv, C) / np.sqrt(kv * C), dtype)
+    b, _ = _q(torch.randn(K) * 0.1, dtype)
+    for what, a, bias, tr, table, M in (("forward", x, b, False, pf, pf.shape[1]),
+                                        ("dgrad", None, None, True, pb, idx.shape[0])):
+        if a is None:
+            a, _ = _q(torch.randn(pf.shape[1], K), dtype)
+        outs = _orders(a, w, bias, tr, table, M)
+        ref = outs[("natural", True)]
+        for key, o in outs.items():
+            assert torch.equal(o, ref), f"{what} {key} differs from the natural planned GEMM"
+    if case == "sparse_wide":
+        variant = getattr(pf, "_spconv_triton_order")[1]
+        plan = variant[2]
+        assert gemm.plan_overflow_count(plan) > 0, "the case must exercise overflow tiles"
+        np.testing.assert_array_equal(variant[1].cpu().numpy(),
+                                      pf.cpu().numpy()[:, variant[0].cpu().numpy()])
+
+
+def test_auto_row_order_decision():
+    """auto: only wide layers on tables whose natural tiles are mostly empty
+    are reordered; narrow layers never read the table statistics."""
+    from spconv_triton.pytorch._impl import gemm
+
+    rng = np.random.default_rng(8)
+    # (voxels, grid, reordered): 30000 in 100^3 has 1.7 pairs per row, yet
+    # nearly every offset has a pair in each natural tile (6.5 % of the MFMA
+    # work is on pairs) and the mask order cuts the work to 23 %; in 40^3 the
+    # mask order only cuts it to 67 %; 20^3 is dense (67 % on pairs); in
+    # 200^3 rows are isolated, so natural tiles already hold only the centre
+    # offset (30 % on pairs)
+    for n, grid, sparse in ((30000, 100, True), (6000, 40, False), (6000, 20, False),
+                            (3000, 200, False)):
+        idx = rand_indices(rng, 1, [grid] * 3, n)
+        pf = _tables(idx, 1, [grid] * 3, [3] * 3, [1] * 3, [1] * 3, True)[2]
+        assert gemm.row_order_variant(pf, n, 64 * 64) is None
+        assert getattr(pf, "_spconv_triton_order", None) is None, "narrow layers decide nothing"
+        variant = gemm.row_order_variant(pf, n, 128 * 128)
+        assert (variant is not None) == sparse
+        if sparse:
+            assert gemm.row_order_variant(pf, n, 64 * 64) is variant, "decision is memoised"
