@@ -127,9 +127,9 @@ def gather_plan(pairs: torch.Tensor, n_src: int):
 #: whose rows do not fit in LDS are gathered directly).  "auto": natural,
 #: unless the layer is wide (C * K >= ORDER_MIN_WORK), the natural tiles spend
 #: less than ORDER_MAX_EFFICIENCY of their MFMA work on pairs, and the mask
-#: order cuts that work to at most ORDER_MAX_WORK_RATIO of it.  The checks read
-#: counters back once per table (one or two stream synchronizations).  Every
-#: order gives bit-identical results.
+#: order cuts that work to at most ORDER_MAX_WORK_RATIO of it; only tables
+#: that wide layers use more than once are looked at (see row_order_variant).
+#: Every order gives bit-identical results.
 ROW_ORDER = os.environ.get("SPCONV_GEMM_ROW_ORDER", "auto")
 ORDER_MIN_WORK = 128 * 128
 ORDER_MAX_EFFICIENCY = 0.2
@@ -137,15 +137,19 @@ ORDER_MAX_WORK_RATIO = 0.35
 _PLAN_MAX_KV = 64  # kv range of the gather plans (sp_gather_plan_bytes)
 
 
-def table_stats(pairs: torch.Tensor, n_src: int) -> tuple[int, int, int]:
-    """(pairs, live (256-row tile, offset) pairs, live (64-row block, offset)
-    pairs) of a [kv, M] table in its own row order (``sp_table_stats``).
-    Reading them synchronizes."""
+def _launch_table_stats(pairs: torch.Tensor, n_src: int) -> torch.Tensor:
     kv, M = pairs.shape
     stats = torch.zeros(3, dtype=torch.int64, device=pairs.device)
     _lib.check(_lib.lib().sp_table_stats(_lib.ptr(pairs), kv, M, int(n_src), _lib.ptr(stats),
                                          _lib.stream_of(pairs.device)), "sp_table_stats")
-    return tuple(int(v) for v in stats.cpu())
+    return stats
+
+
+def table_stats(pairs: torch.Tensor, n_src: int) -> tuple[int, int, int]:
+    """(pairs, live (256-row tile, offset) pairs, live (64-row block, offset)
+    pairs) of a [kv, M] table in its own row order (``sp_table_stats``).
+    Reading them synchronizes."""
+    return tuple(int(v) for v in _launch_table_stats(pairs, n_src).cpu())
 
 
 def mask_order(pairs: torch.Tensor) -> torch.Tensor:
@@ -170,37 +174,47 @@ def permute_table(pairs: torch.Tensor, order: torch.Tensor) -> torch.Tensor:
 def row_order_variant(pairs: torch.Tensor, n_src: int, work: int):
     """(order, permuted table, its gather plan or None) when a GEMM of
     ``work`` = C * K on this table should take its rows in mask order (see
-    ROW_ORDER), else None.  Memoised on the table tensor like its plan."""
+    ROW_ORDER), else None.
+
+    In auto mode only tables that wide layers use more than once are looked
+    at: the first wide call on a table runs in natural order and launches
+    nothing (a table rebuilt every step costs nothing); the second reads the
+    table's statistics back (a stream synchronization) and, when they pass,
+    sorts the masks, permutes the table and reads the permuted table's
+    statistics (a second one).  The outcome is memoised on the table tensor
+    (like its plan) and recomputed if the table changes."""
     mode = ROW_ORDER
     if mode == "natural":
         return None
     if mode not in ("auto", "mask"):
         raise ValueError(f"SPCONV_GEMM_ROW_ORDER must be auto, natural or mask, not {mode!r}")
+    kv, M = pairs.shape
+    if M == 0:
+        return None
     stamp = (int(n_src), pairs._version, pairs.data_ptr(), mode)
     cached = getattr(pairs, "_spconv_triton_order", None)
-    if cached is not None and cached[0] == stamp:
-        return cached[1]
-    kv, M = pairs.shape
+    step = cached[1] if cached is not None and cached[0] == stamp else "start"
+    if isinstance(step, tuple):
+        return step  # a settled mask order serves every layer on the table
+    if step == "natural" or (mode == "auto" and work < ORDER_MIN_WORK):
+        return None  # narrow layers never start the decision
+    if mode == "auto" and step == "start":
+        pairs._spconv_triton_order = (stamp, "seen")
+        return None
 
     def mfma_rows(stats):  # rows the GEMM multiplies: per live tile or wave offset
         return 256 * stats[1] if kv <= _PLAN_MAX_KV else 64 * stats[2]
 
-    if mode == "auto":
-        if work < ORDER_MIN_WORK or M == 0:
-            return None  # not decided: a wider layer on this table may still reorder
-        natural = table_stats(pairs, n_src)
-        done = mfma_rows(natural)
-        if done == 0 or natural[0] >= ORDER_MAX_EFFICIENCY * done:
-            pairs._spconv_triton_order = (stamp, None)
-            return None
-    order = mask_order(pairs)
-    perm = permute_table(pairs, order)
-    if mode == "auto" and mfma_rows(table_stats(perm, n_src)) > ORDER_MAX_WORK_RATIO * done:
-        pairs._spconv_triton_order = (stamp, None)
-        return None
-    plan = gather_plan(perm, n_src) if USE_GATHER_PLAN else None
-    variant = (order, perm, plan)
-    pairs._spconv_triton_order = (stamp, variant)
+    variant = None
+    natural = table_stats(pairs, n_src) if mode == "auto" else None
+    done = mfma_rows(natural) if natural is not None else 0
+    if mode == "mask" or (done > 0 and natural[0] < ORDER_MAX_EFFICIENCY * done):
+        order = mask_order(pairs)
+        perm = permute_table(pairs, order)
+        if mode == "mask" or mfma_rows(table_stats(perm, n_src)) <= ORDER_MAX_WORK_RATIO * done:
+            plan = gather_plan(perm, n_src) if USE_GATHER_PLAN else None
+            variant = (order, perm, plan)
+    pairs._spconv_triton_order = (stamp, variant if variant is not None else "natural")
     return variant
 
 

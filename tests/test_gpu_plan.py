@@ -320,7 +320,8 @@ def test_mask_row_order_bit_identical(case, dtype):
 
 def test_auto_row_order_decision():
     """auto: only wide layers on tables whose natural tiles are mostly empty
-    are reordered; narrow layers never read the table statistics."""
+    are reordered.  Narrow layers never look at the table, and the first wide
+    call on a table launches nothing; the second decides."""
     from spconv_triton.pytorch._impl import gemm
 
     rng = np.random.default_rng(8)
@@ -336,7 +337,11 @@ def test_auto_row_order_decision():
         pf = _tables(idx, 1, [grid] * 3, [3] * 3, [1] * 3, [1] * 3, True)[2]
         assert gemm.row_order_variant(pf, n, 64 * 64) is None
         assert getattr(pf, "_spconv_triton_order", None) is None, "narrow layers decide nothing"
+        assert gemm.row_order_variant(pf, n, 128 * 128) is None
+        assert pf._spconv_triton_order[1] == "seen", "a first wide call launches nothing"
         variant = gemm.row_order_variant(pf, n, 128 * 128)
         assert (variant is not None) == sparse
         if sparse:
             assert gemm.row_order_variant(pf, n, 64 * 64) is variant, "decision is memoised"
+        else:
+            assert pf._spconv_triton_order[1] == "natural"
