@@ -1,0 +1,234 @@
+"""Timings of the benchmark configurations other than the headline one.
+
+``bench.py`` measures the headline layer (one JSON line, the driver's
+contract).  This script times the other configurations of the baseline at
+their stated sizes, on synthetic clouds from ``bench_data`` and random
+weights, and prints one JSON object per configuration:
+
+* ``encoder``: VoxelBackBone8x-style encoder, fp16 eval, batch 4 x ~20k
+  LiDAR voxels in [41, 1600, 1408]; rulebooks rebuilt every pass;
+* ``resunet``: sparse ResUNet training step (forward + backward), fp16
+  autocast, batch 2 x ~120k voxels in [128, 2048, 2048]; rulebooks rebuilt
+  every step;
+* ``subm4d``: SubMConv4d 3^4, 128 -> 128 fp16, ~500k voxels in
+  [64, 512, 512, 512], rulebook cached;
+* ``wide``: SubMConv3d 256 -> 256 fp16, 400k voxels of a 1024^3 surface
+  cloud, rulebook cached.
+
+Usage: ``python bench_configs.py [--config NAME ...] [--reps R]``.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "spconv-triton_amd"))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+from bench_data import lidar_cloud, surface_cloud, urban_cloud  # noqa: E402
+
+DEV = torch.device("cuda:0")
+
+# (kind, cin, cout, kernel, [stride, padding,] indice_key); every conv is
+# followed by BatchNorm + ReLU
+ENCODER = [
+    ("subm", 4, 16, 3, "subm1"),
+    ("conv", 16, 32, 3, 2, 1, "spconv2"),
+    ("subm", 32, 32, 3, "subm2"),
+    ("subm", 32, 32, 3, "subm2"),
+    ("conv", 32, 64, 3, 2, 1, "spconv3"),
+    ("subm", 64, 64, 3, "subm3"),
+    ("subm", 64, 64, 3, "subm3"),
+    ("conv", 64, 64, 3, 2, (0, 1, 1), "spconv4"),
+    ("subm", 64, 64, 3, "subm4"),
+    ("subm", 64, 64, 3, "subm4"),
+    ("conv", 64, 128, (3, 1, 1), (2, 1, 1), 0, "spconv_down2"),
+]
+
+RESUNET = {
+    "stem": [("subm", 4, 32, 3, "s0")],
+    "e1": [("conv", 32, 64, 2, 2, 0, "d1"), ("subm", 64, 64, 3, "s1")],
+    "e2": [("pool", 2, 2, "p2"), ("subm", 64, 128, 3, "s2")],
+    "e3": [("conv", 128, 256, 2, 2, 0, "d3"), ("subm", 256, 256, 3, "s3")],
+    "u3": [("inv", 256, 128, 2, "d3")],
+    "m2": [("subm", 256, 128, 3, "s2")],
+    "u2": [("inv", 128, 64, 2, "p2")],
+    "m1": [("subm", 128, 64, 3, "s1")],
+    "u1": [("inv", 64, 32, 2, "d1")],
+    "m0": [("subm", 64, 32, 3, "s0")],
+}
+
+
+def build(blocks):
+    import spconv_triton.pytorch as spconv
+
+    mods = []
+    for blk in blocks:
+        kind = blk[0]
+        if kind == "pool":
+            _, k, stride, key = blk
+            mods.append(spconv.SparseMaxPool3d(k, stride, indice_key=key))
+            continue
+        if kind == "subm":
+            _, cin, cout, k, key = blk
+            conv = spconv.SubMConv3d(cin, cout, k, padding=1, bias=False, indice_key=key)
+        elif kind == "conv":
+            _, cin, cout, k, stride, pad, key = blk
+            conv = spconv.SparseConv3d(cin, cout, k, stride=stride, padding=pad, bias=False,
+                                       indice_key=key)
+        else:
+            _, cin, cout, k, key = blk
+            conv = spconv.SparseInverseConv3d(cin, cout, k, bias=False, indice_key=key)
+        mods += [conv, torch.nn.BatchNorm1d(cout), torch.nn.ReLU()]
+    return spconv.SparseSequential(*mods).to(DEV)
+
+
+def median_ms(fn, reps):
+    ts = []
+    for _ in range(reps):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(ts)
+
+
+def cfg_encoder(reps):
+    import spconv_triton.pytorch as spconv
+
+    shape = [41, 1600, 1408]
+    idx = lidar_cloud(20000, batch=4, seed=0, shape=shape)
+    it = torch.from_numpy(idx).to(DEV)
+    feats = torch.rand(idx.shape[0], 4, device=DEV).half()
+    net = build(ENCODER).half().eval()
+
+    def step():
+        with torch.no_grad():
+            return net(spconv.SparseConvTensor(feats, it, shape, 4))
+
+    for _ in range(3):
+        step()
+    return {"voxels": int(idx.shape[0]), "median_ms": median_ms(step, reps),
+            "what": "encoder forward, fp16 eval, rulebooks rebuilt every pass"}
+
+
+def cfg_resunet(reps):
+    import spconv_triton.pytorch as spconv
+
+    shape = [128, 2048, 2048]
+    idx = urban_cloud(120000, batch=2, seed=9, shape=shape)
+    it = torch.from_numpy(idx).to(DEV)
+    n = idx.shape[0]
+    feats = torch.rand(n, 4, device=DEV)
+    labels = torch.randint(0, 20, (n,), device=DEV)
+    parts = {k: build(v).train() for k, v in RESUNET.items()}
+    head = spconv.SubMConv3d(32, 20, 1, bias=True).to(DEV)
+    join = spconv.JoinTable()
+    params = [p for m in parts.values() for p in m.parameters()] + list(head.parameters())
+
+    def step():
+        x = spconv.SparseConvTensor(feats.clone().requires_grad_(True), it, shape, 2)
+        with torch.autocast("cuda", dtype=torch.float16):
+            s0 = parts["stem"](x)
+            s1 = parts["e1"](s0)
+            s2 = parts["e2"](s1)
+            s3 = parts["e3"](s2)
+            u = parts["m2"](join([parts["u3"](s3), s2]))
+            u = parts["m1"](join([parts["u2"](u), s1]))
+            u = parts["m0"](join([parts["u1"](u), s0]))
+            logits = head(u)
+            loss = torch.nn.functional.cross_entropy(logits.features.float(), labels)
+        loss.backward()
+        for p in params:
+            p.grad = None
+
+    for _ in range(3):
+        step()
+    return {"voxels": int(n), "median_ms": median_ms(step, reps),
+            "what": "training step (forward + backward), fp16 autocast, rulebooks rebuilt"}
+
+
+def _cached_layer(conv, idx, shape, C, reps):
+    import spconv_triton.pytorch as spconv
+
+    it = torch.from_numpy(idx).to(DEV)
+    feats = torch.randn(idx.shape[0], C, device=DEV).half()
+    bs = int(idx[:, 0].max()) + 1
+    with torch.no_grad():
+        y = conv(spconv.SparseConvTensor(feats, it, shape, bs))
+        xc = spconv.SparseConvTensor(feats, it, shape, bs, indice_dict=y.indice_dict)
+        for _ in range(5):
+            conv(xc)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = 10 * reps
+        e0.record()
+        for _ in range(n):
+            conv(xc)
+        e1.record()
+        torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
+def cfg_subm4d(reps):
+    import spconv_triton.pytorch as spconv
+
+    # 64 time steps of a slowly drifting surface cloud in 512^3
+    rng = np.random.default_rng(0)
+    base = surface_cloud(8000, 512, seed=3)[:, 1:].astype(np.int64)
+    rows = []
+    for t in range(64):
+        c = np.clip(base + (np.array([t // 8, t // 16, t // 4]) % 512), 0, 511)
+        c = c[rng.random(c.shape[0]) < 0.98]
+        rows.append(np.concatenate([np.zeros((c.shape[0], 1), np.int64),
+                                    np.full((c.shape[0], 1), t), c], 1))
+    idx = np.unique(np.concatenate(rows).astype(np.int32), axis=0)
+    torch.manual_seed(0)
+    conv = spconv.SubMConv4d(128, 128, 3, padding=1, bias=False, indice_key="k").to(DEV)
+    ms = _cached_layer(conv.half().eval(), idx, [64, 512, 512, 512], 128, reps)
+    return {"voxels": int(idx.shape[0]), "median_ms": ms,
+            "what": "SubMConv4d 3^4 128->128 fp16 forward, rulebook cached (mean)"}
+
+
+def cfg_wide(reps):
+    import spconv_triton.pytorch as spconv
+
+    idx = surface_cloud(400000, 1024, seed=0)
+    torch.manual_seed(0)
+    conv = spconv.SubMConv3d(256, 256, 3, padding=1, bias=False, indice_key="k").to(DEV)
+    ms = _cached_layer(conv.half().eval(), idx, [1024] * 3, 256, reps)
+    return {"voxels": int(idx.shape[0]), "median_ms": ms,
+            "what": "SubMConv3d 256->256 fp16 forward, 1024^3 surface cloud, rulebook cached (mean)"}
+
+
+CONFIGS = {"encoder": cfg_encoder, "resunet": cfg_resunet, "subm4d": cfg_subm4d,
+           "wide": cfg_wide}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--config", nargs="*", choices=sorted(CONFIGS), default=list(CONFIGS))
+    ap.add_argument("--reps", type=int, default=10)
+    args = ap.parse_args()
+    if not torch.cuda.is_available():
+        print("bench_configs.py needs a GPU", file=sys.stderr)
+        return 2
+    for name in args.config:
+        res = CONFIGS[name](args.reps)
+        print(json.dumps({"config": name, **{k: (round(v, 4) if isinstance(v, float) else v)
+                                            for k, v in res.items()}}), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -220,7 +220,7 @@ int sp_conv_gemm_ordered(const void* a, int32_t dtype, int64_t n_src, const void
 int sp_permute_table(const int32_t* pairs, int64_t kv, int64_t M, const int32_t* order,
                      int32_t* out, void* stream);
 
-/* Work statistics of a gather table [kv, M] in its own row order, added into
+/* Work statistics of a gather table [kv, M] (kv <= 512) in its own row order, added into
  * stats[0..2] (int64, zeroed by the caller): the pairs (entries in
  * 0..n_src-1), the (256-row tile, offset) pairs with at least one pair and
  * the (64-row block, offset) pairs with at least one pair.  pairs / (256 *

@@ -256,28 +256,65 @@ __global__ __launch_bounds__(256) void plan_overflow_kernel(const int32_t* __res
 // row order, they give the share of a GEMM's MFMA work spent on pairs: the
 // staged kernel runs 256 rows per live tile offset, the direct one 64 rows
 // per live wave offset.
+// A workgroup takes tiles blockIdx.x, blockIdx.x + gridDim.x, ... and adds
+// its totals with one atomic per counter (a few hundred atomics in all: one
+// per wave and tile serialised on the three addresses for ~175 us).
 __global__ __launch_bounds__(256) void table_stats_kernel(const int32_t* __restrict__ pairs,
                                                           int64_t M, int kv, int64_t n_src,
+                                                          int64_t ntiles,
                                                           unsigned long long* __restrict__ stats) {
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int64_t r = int64_t(blockIdx.x) * 256 + tid;
+  constexpr int kMaxWords = 16;  // offsets counted per launch: kv <= 512
+  __shared__ uint32_t s_or[kMaxWords];
+  __shared__ uint32_t s_sum[2][4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nw = (kv + 31) / 32;
   uint32_t npair = 0, wave_live = 0, tile_live = 0;
-  for (int k = 0; k < kv; ++k) {
-    bool ok = false;
-    if (r < M) {
-      const int32_t x = pairs[int64_t(k) * M + r];
-      ok = x >= 0 && x < n_src;
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t r = tile * 256 + tid;
+    if (tid < kMaxWords) s_or[tid] = 0u;
+    __syncthreads();
+    for (int w = 0; w < nw; ++w) {
+      // the row's validity bits for offsets 32 w .. 32 w + 31, loads 8 at a time
+      uint32_t bits = 0;
+      for (int j0 = 0; j0 < 32; j0 += 8) {
+        int32_t x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int k = 32 * w + j0 + j;
+          x[j] = (r < M && k < kv) ? pairs[int64_t(k) * M + r] : -1;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (x[j] >= 0 && x[j] < n_src) bits |= 1u << (j0 + j);
+      }
+      npair += uint32_t(__builtin_popcount(bits));
+      uint32_t any = bits;  // offsets live in the wave
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) any |= __shfl_xor(any, off, 64);
+      wave_live += uint32_t(__builtin_popcount(any));
+      if (lane == 0) atomicOr(&s_or[w], any);
     }
-    npair += ok ? 1u : 0u;
-    wave_live += __builtin_amdgcn_ballot_w64(ok) != 0 ? 1u : 0u;
-    tile_live += __syncthreads_or(ok) ? 1u : 0u;
+    __syncthreads();
+    if (tid == 0)
+      for (int w = 0; w < nw; ++w) tile_live += uint32_t(__builtin_popcount(s_or[w]));
+    __syncthreads();  // s_or is cleared for the next tile
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) npair += __shfl_xor(npair, off, 64);
   if (lane == 0) {
-    atomicAdd(&stats[0], (unsigned long long)npair);
-    atomicAdd(&stats[2], (unsigned long long)wave_live);
-    if (tid == 0) atomicAdd(&stats[1], (unsigned long long)tile_live);
+    s_sum[0][wave] = npair;
+    s_sum[1][wave] = wave_live;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    unsigned long long a = 0, b = 0;
+    for (int w = 0; w < 4; ++w) {
+      a += s_sum[0][w];
+      b += s_sum[1][w];
+    }
+    atomicAdd(&stats[0], a);
+    atomicAdd(&stats[1], (unsigned long long)tile_live);
+    atomicAdd(&stats[2], b);
   }
 }
 
@@ -359,9 +396,11 @@ int sp_table_stats(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_src, i
   if (M == 0) return SP_OK;
   SP_CHECK_ARG(pairs && stats, "table stats: null pointer");
   const int64_t nt = cdiv(M, int64_t(256));
-  SP_CHECK_ARG(nt <= kMaxGridX && kv < 65536, "table stats: too many rows");
-  table_stats_kernel<<<unsigned(nt), 256, 0, as_stream(stream)>>>(
-      pairs, M, int(kv), n_src, reinterpret_cast<unsigned long long*>(stats));
+  SP_CHECK_ARG(nt <= kMaxGridX, "table stats: too many rows");
+  SP_CHECK_ARG(kv <= 512, "table stats: kv=%lld above 512", (long long)kv);
+  const unsigned grid = unsigned(nt < 512 ? nt : 512);
+  table_stats_kernel<<<grid, 256, 0, as_stream(stream)>>>(
+      pairs, M, int(kv), n_src, nt, reinterpret_cast<unsigned long long*>(stats));
   SP_LAUNCHED();
   return SP_OK;
 }

@@ -135,6 +135,7 @@ ORDER_MIN_WORK = 128 * 128
 ORDER_MAX_EFFICIENCY = 0.2
 ORDER_MAX_WORK_RATIO = 0.35
 _PLAN_MAX_KV = 64  # kv range of the gather plans (sp_gather_plan_bytes)
+_STATS_MAX_KV = 512  # kv range of sp_table_stats
 
 
 def _launch_table_stats(pairs: torch.Tensor, n_src: int) -> torch.Tensor:
@@ -196,7 +197,7 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int):
     step = cached[1] if cached is not None and cached[0] == stamp else "start"
     if isinstance(step, tuple):
         return step  # a settled mask order serves every layer on the table
-    if step == "natural" or (mode == "auto" and work < ORDER_MIN_WORK):
+    if step == "natural" or (mode == "auto" and (work < ORDER_MIN_WORK or kv > _STATS_MAX_KV)):
         return None  # narrow layers never start the decision
     if mode == "auto" and step == "start":
         pairs._spconv_triton_order = (stamp, "seen")
