@@ -183,7 +183,9 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int):
     table's statistics back (a stream synchronization) and, when they pass,
     sorts the masks, permutes the table and reads the permuted table's
     statistics (a second one).  The outcome is memoised on the table tensor
-    (like its plan) and recomputed if the table changes."""
+    (like its plan) and recomputed if the table changes.  Calls made while
+    the stream is being captured into a graph use a settled order but never
+    advance the decision."""
     mode = ROW_ORDER
     if mode == "natural":
         return None
@@ -199,6 +201,8 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int):
         return step  # a settled mask order serves every layer on the table
     if step == "natural" or (mode == "auto" and (work < ORDER_MIN_WORK or kv > _STATS_MAX_KV)):
         return None  # narrow layers never start the decision
+    if torch.cuda.is_current_stream_capturing():
+        return None  # a graph being captured must not synchronize: decide on a later call
     if mode == "auto" and step == "start":
         pairs._spconv_triton_order = (stamp, "seen")
         return None

@@ -345,3 +345,37 @@ def test_auto_row_order_decision():
             assert gemm.row_order_variant(pf, n, 64 * 64) is variant, "decision is memoised"
         else:
             assert pf._spconv_triton_order[1] == "natural"
+
+
+def test_row_order_decision_waits_out_graph_capture():
+    """A wide sparse layer captured into a HIP graph at its second call (when
+    the decision would read counters back) captures the natural-order GEMM;
+    its replays equal the eager result, and the next eager call settles the
+    mask order with the same result."""
+    from spconv_triton.pytorch._impl import gemm
+
+    rng = np.random.default_rng(8)
+    n, grid, C, K = 30000, 100, 128, 128
+    idx = rand_indices(rng, 1, [grid] * 3, n)
+    pf = _tables(idx, 1, [grid] * 3, [3] * 3, [1] * 3, [1] * 3, True)[2]
+    torch.manual_seed(2)
+    x = torch.randn(n, C, device=DEV).half()
+    w = (torch.randn(K, 27, C, device=DEV) / np.sqrt(27 * C)).half()
+    eager = gemm.conv_forward(x, w, pf, n)  # first wide call: nothing launched
+    assert pf._spconv_triton_order[1] == "seen"
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            out = gemm.conv_forward(x, w, pf, n)
+    torch.cuda.current_stream().wait_stream(s)
+    assert pf._spconv_triton_order[1] == "seen", "capture must not advance the decision"
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+    settled = gemm.conv_forward(x, w, pf, n)
+    assert isinstance(pf._spconv_triton_order[1], tuple), "the next eager call settles"
+    assert torch.equal(settled, eager)
