@@ -188,14 +188,17 @@ __host__ __device__ constexpr uint32_t epi_bytes(uint32_t out_size) {
 // 64 * epi_pitch bytes, free once the caller has passed a barrier) and is
 // stored as whole rows, otherwise element by element.  Rows past M fall
 // outside the output buffer and their stores are dropped.  With a row order
-// (nullable), tile row `slot` is output row order[slot].
+// (nullable), tile row `slot` is output row order[slot]; an entry outside
+// 0..M-1 is treated as a row past M (its stores are dropped).
 template <typename OutT>
 __device__ __forceinline__ void store_tile(const floatx16 (&acc)[2][2], const float* bias,
                                            __amdgpu_buffer_rsrc_t ro, unsigned char* stage,
                                            int64_t slot0, int n0, int64_t M, int N, int lane,
                                            const int32_t* __restrict__ order) {
   auto out_row = [&](int64_t slot) -> int64_t {
-    return (order && slot < M) ? int64_t(order[slot]) : slot;
+    if (!order || slot >= M) return slot;
+    const int64_t r = order[slot];
+    return (r >= 0 && r < M) ? r : M;
   };
   constexpr uint32_t OS = sizeof(OutT);
   constexpr int kPer16 = int(16 / OS);  // output elements per 16-byte piece
@@ -225,10 +228,8 @@ __device__ __forceinline__ void store_tile(const floatx16 (&acc)[2][2], const fl
       const int r = pr + j * kRowsPerPass;
       const uint4 v =
           *reinterpret_cast<const uint4*>(stage + uint32_t(r) * pitch + uint32_t(pc) * 16u);
-      const int64_t slot = slot0 + r;
-      const int64_t row = out_row(slot);
-      const uint32_t off =
-          (slot < M && col < N) ? uint32_t((row * N + col) * int64_t(OS)) : kOob;
+      const int64_t row = out_row(slot0 + r);
+      const uint32_t off = (row < M && col < N) ? uint32_t((row * N + col) * int64_t(OS)) : kOob;
       __builtin_amdgcn_raw_buffer_store_b128(
           __builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, v), ro, off, 0, 0);
     }
@@ -242,10 +243,9 @@ __device__ __forceinline__ void store_tile(const floatx16 (&acc)[2][2], const fl
     for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int64_t slot = slot0 + mt * 32 + 8 * (i / 4) + 4 * h + (i % 4);
-        const int64_t row = out_row(slot);
+        const int64_t row = out_row(slot0 + mt * 32 + 8 * (i / 4) + 4 * h + (i % 4));
         const uint32_t off =
-            (slot < M && col < N) ? uint32_t((row * N + col) * int64_t(OS)) : kOob;
+            (row < M && col < N) ? uint32_t((row * N + col) * int64_t(OS)) : kOob;
         buf_store<OutT>(from_f32<OutT>(acc[mt][nt][i] + bv), ro, off);
       }
     }
@@ -424,14 +424,17 @@ __device__ __forceinline__ void direct_tile(const T* __restrict__ A, const T* __
 }
 
 // Every tile of an unplanned call, one workgroup per (tile, 64 columns).
-template <typename T, typename OutT, bool VEC>
+// ORDERED instances take tile rows through `order` (the natural ones ignore
+// the argument, so the pointer costs them no registers).
+template <typename T, typename OutT, bool VEC, bool ORDERED>
 __global__ __launch_bounds__(256, 2) void gather_gemm_direct(
     const T* __restrict__ A, const T* __restrict__ Bt, const int32_t* __restrict__ pairs,
     const int32_t* __restrict__ order, const float* __restrict__ bias, OutT* __restrict__ out,
     GemmBufs nb, int64_t n_src, int64_t M, int N, int R, int Rp, int kv) {
   extern __shared__ __align__(16) unsigned char smem[];
   direct_tile<T, OutT, VEC>(A, Bt, pairs, bias, out, nb, n_src, M, N, R, Rp, kv,
-                            xcd_tile(blockIdx.x, gridDim.x), int(blockIdx.y) * 64, smem, order);
+                            xcd_tile(blockIdx.x, gridDim.x), int(blockIdx.y) * 64, smem,
+                            ORDERED ? order : nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -460,13 +463,15 @@ __host__ __device__ inline StagedLds staged_lds(int E, uint32_t out_size) {
 }
 
 // Every tile of a planned call (kv <= kPlanMaxKv): staged when its distinct
-// rows fit in LDS, else (an overflow tile) by the direct path.
-template <typename T, typename OutT, bool VEC>
+// rows fit in LDS, else (an overflow tile) by the direct path.  ORDERED as
+// for the direct kernel.
+template <typename T, typename OutT, bool VEC, bool ORDERED>
 __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
     const T* __restrict__ A, const T* __restrict__ Bt, const int32_t* __restrict__ pairs,
-    const int32_t* __restrict__ order, PlanDev plan, const float* __restrict__ bias,
+    const int32_t* __restrict__ order_arg, PlanDev plan, const float* __restrict__ bias,
     OutT* __restrict__ out, GemmBufs nb, int64_t n_src, int64_t M, int N, int R, int Rp,
     int kv) {
+  const int32_t* __restrict__ order = ORDERED ? order_arg : nullptr;
   using frag = typename Mfma<T>::frag;
   constexpr int V = Mfma<T>::V;
   constexpr uint32_t ES = sizeof(T);

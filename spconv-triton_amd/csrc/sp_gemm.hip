@@ -414,10 +414,12 @@ static int launch_direct(dim3 grid, hipStream_t s, const T* A, const T* bt, cons
                          OutT* o, GemmBufs nb, const GemmCall& c) {
   const int G = c.kv < kGroupOffsets ? c.kv : kGroupOffsets;
   const uint32_t lds = direct_lds(G + kPad, uint32_t(sizeof(OutT))).total;
-  auto kern = gather_gemm_direct<T, OutT, VEC>;
-  static bool attr_set = false;
+  auto kern = c.order ? gather_gemm_direct<T, OutT, VEC, true>
+                      : gather_gemm_direct<T, OutT, VEC, false>;
+  static bool attr_set[2] = {false, false};  // per kernel instance
   int rc = allow_lds(reinterpret_cast<const void*>(kern),
-                     direct_lds(kGroupOffsets + kPad, uint32_t(sizeof(OutT))).total, attr_set);
+                     direct_lds(kGroupOffsets + kPad, uint32_t(sizeof(OutT))).total,
+                     attr_set[c.order ? 1 : 0]);
   if (rc) return rc;
   kern<<<grid, 256, lds, s>>>(A, bt, pairs, c.order, c.bias, o, nb, c.n_src, c.M, c.N, c.R, c.Rp,
                               c.kv);
@@ -438,10 +440,12 @@ template <typename T, typename OutT, bool VEC>
 static int launch_staged(dim3 grid, hipStream_t s, const T* A, const T* bt, const int32_t* pairs,
                          OutT* o, GemmBufs nb, const GemmCall& c) {
   const uint32_t lds = staged_kernel_lds(c.plan.E, c.kv, uint32_t(sizeof(OutT)));
-  auto kern = gather_gemm_staged<T, OutT, VEC>;
-  static bool attr_set = false;
+  auto kern = c.order ? gather_gemm_staged<T, OutT, VEC, true>
+                      : gather_gemm_staged<T, OutT, VEC, false>;
+  static bool attr_set[2] = {false, false};  // per kernel instance
   int rc = allow_lds(reinterpret_cast<const void*>(kern),
-                     staged_kernel_lds(kPlanMaxKv, kPlanMaxKv, uint32_t(sizeof(OutT))), attr_set);
+                     staged_kernel_lds(kPlanMaxKv, kPlanMaxKv, uint32_t(sizeof(OutT))),
+                     attr_set[c.order ? 1 : 0]);
   if (rc) return rc;
   kern<<<grid, 256, lds, s>>>(A, bt, pairs, c.order, c.plan, c.bias, o, nb, c.n_src, c.M, c.N,
                               c.R, c.Rp, c.kv);
