@@ -186,9 +186,22 @@ __global__ __launch_bounds__(256) void wgrad_partial(
   constexpr int V = MF::V;
   constexpr int KSTEP = MF::KSTEP;
   constexpr uint32_t ES = sizeof(T);
-  constexpr int STAGE = S::kStage, PITCH = S::kPitch, NV = S::kNv, MT = S::kMt;
+  constexpr int STAGE = S::kStage, NV = S::kNv, MT = S::kMt;
+  // 16-bit rows with whole 16-byte vectors are gathered coalesced: the four
+  // lanes of a pair read 64 contiguous bytes of its row per load (16 rows per
+  // load instruction, against 64 rows of one 16-byte piece each otherwise).
+  // The 8-pair columns of their channel-major LDS rows are XOR-swizzled by
+  // channel bit 4, so that both the staging writes and the MFMA fragment
+  // reads are free of bank conflicts; the swizzle is constant over a thread's
+  // 8 channels of a vector, so the write addresses stay base + immediate.
+  constexpr bool COAL = VEC && sizeof(T) == 2 && STAGE == 128;
+  constexpr int PITCH = S::kPitch;
   __shared__ __align__(16) T Xs[BW][PITCH];
   __shared__ __align__(16) T Gs[BW][PITCH];
+  // element offset of pair p within channel row c
+  auto elem = [](int c, int p) -> int {
+    return COAL ? ((((p >> 3) ^ (((c >> 4) & 1) << 2)) << 3) | (p & 7)) : p;
+  };
 
   const int k = blockIdx.x / splits;
   const int split = blockIdx.x % splits;
@@ -197,8 +210,12 @@ __global__ __launch_bounds__(256) void wgrad_partial(
   const int wave = tid >> 6, lane = tid & 63;
   const int h = lane >> 5, l32 = lane & 31;
   const int ctile = (wave >> 1) * (BW / 2), ntile = (wave & 1) * (BW / 2);
-  // staging role: pairs 2 pp and 2 pp + 1 of a stage, channels kCh q .. kCh q + kCh - 1
-  const int pp = tid % S::kPairRows, q = tid / S::kPairRows;
+  // staging role: pairs 2 pp and 2 pp + 1 of a stage and NV vectors of V
+  // channels each, vector j at channel ch_of(j): kCh contiguous channels from
+  // kCh q, or (COAL) channels 4 V j + V ql of a 4-lane group per pair pair
+  const int pp = COAL ? 16 * wave + (lane >> 2) : tid % S::kPairRows;
+  const int q = COAL ? (lane & 3) : tid / S::kPairRows;
+  auto ch_of = [&](int j) -> int { return COAL ? j * 4 * V + q * V : q * S::kCh + j * V; };
 
   const int64_t cnt = counts[k];
   const int64_t chunk = (cnt + splits - 1) / splits;
@@ -231,7 +248,7 @@ __global__ __launch_bounds__(256) void wgrad_partial(
     for (int e = 0; e < 2; ++e)
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
-        const int cx = c0 + q * S::kCh + j * V, nx = n0 + q * S::kCh + j * V;
+        const int cx = c0 + ch_of(j), nx = n0 + ch_of(j);
         if (VEC) {
           xv[e][j] = buf_frag<T>(rx, row_off(iv[e], cx, C, C));
           gv[e][j] = buf_frag<T>(rg, row_off(ov[e], nx, K, K));
@@ -250,11 +267,12 @@ __global__ __launch_bounds__(256) void wgrad_partial(
     for (int j = 0; j < NV; ++j)
 #pragma unroll
       for (int t = 0; t < V; ++t) {
-        const int c = q * S::kCh + j * V + t;
+        const int c = ch_of(j) + t;
+        const int e = elem(c, 2 * pp);
         const T2 xp = {xv[0][j][t], xv[1][j][t]};
         const T2 gp = {gv[0][j][t], gv[1][j][t]};
-        *reinterpret_cast<T2*>(&Xs[c][2 * pp]) = xp;
-        *reinterpret_cast<T2*>(&Gs[c][2 * pp]) = gp;
+        *reinterpret_cast<T2*>(&Xs[c][e]) = xp;
+        *reinterpret_cast<T2*>(&Gs[c][e]) = gp;
       }
   };
 
@@ -288,8 +306,9 @@ __global__ __launch_bounds__(256) void wgrad_partial(
       frag a[MT], b[MT];
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        a[m] = *reinterpret_cast<const frag*>(&Xs[ctile + 32 * m + l32][st + h * V]);
-        b[m] = *reinterpret_cast<const frag*>(&Gs[ntile + 32 * m + l32][st + h * V]);
+        const int ca = ctile + 32 * m + l32, cb = ntile + 32 * m + l32;
+        a[m] = *reinterpret_cast<const frag*>(&Xs[ca][elem(ca, st + h * V)]);
+        b[m] = *reinterpret_cast<const frag*>(&Gs[cb][elem(cb, st + h * V)]);
       }
 #pragma unroll
       for (int mc = 0; mc < MT; ++mc)
