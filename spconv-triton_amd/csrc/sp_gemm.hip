@@ -174,7 +174,9 @@ struct WgShape {
   static_assert(2 * BW * kPitch * sizeof(T) <= 72 * 1024, "wgrad LDS");
 };
 
-template <typename T, bool VEC, int BW>
+// VEC bit 0: X rows are whole 16-byte vectors (C % V == 0, aligned base),
+// bit 1: the same for the G rows; otherwise that tensor is read element-wise.
+template <typename T, int VEC, int BW>
 __global__ __launch_bounds__(256) void wgrad_partial(
     const T* __restrict__ X, int64_t n_in, const T* __restrict__ G, int64_t n_out, int C, int K,
     int kv, const int32_t* __restrict__ in_rows, const int32_t* __restrict__ out_rows,
@@ -187,14 +189,14 @@ __global__ __launch_bounds__(256) void wgrad_partial(
   constexpr int KSTEP = MF::KSTEP;
   constexpr uint32_t ES = sizeof(T);
   constexpr int STAGE = S::kStage, NV = S::kNv, MT = S::kMt;
-  // 16-bit rows with whole 16-byte vectors are gathered coalesced: the four
-  // lanes of a pair read 64 contiguous bytes of its row per load (16 rows per
-  // load instruction, against 64 rows of one 16-byte piece each otherwise).
+  // 16-bit rows are gathered coalesced: the four lanes of a pair read 64
+  // contiguous bytes of its row per load (16 rows per load instruction,
+  // against 64 rows of one 16-byte piece each otherwise).
   // The 8-pair columns of their channel-major LDS rows are XOR-swizzled by
   // channel bit 4, so that both the staging writes and the MFMA fragment
   // reads are free of bank conflicts; the swizzle is constant over a thread's
   // 8 channels of a vector, so the write addresses stay base + immediate.
-  constexpr bool COAL = VEC && sizeof(T) == 2 && STAGE == 128;
+  constexpr bool COAL = sizeof(T) == 2 && STAGE == 128;
   constexpr int PITCH = S::kPitch;
   __shared__ __align__(16) T Xs[BW][PITCH];
   __shared__ __align__(16) T Gs[BW][PITCH];
@@ -249,15 +251,16 @@ __global__ __launch_bounds__(256) void wgrad_partial(
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
         const int cx = c0 + ch_of(j), nx = n0 + ch_of(j);
-        if (VEC) {
+        if (VEC & 1)
           xv[e][j] = buf_frag<T>(rx, row_off(iv[e], cx, C, C));
-          gv[e][j] = buf_frag<T>(rg, row_off(ov[e], nx, K, K));
-        } else {
+        else
           xv[e][j] = buf_frag_elems<T>(rx, iv[e] >= 0 ? uint32_t(int64_t(iv[e]) * C * ES) : kOob,
                                        cx, C);
+        if (VEC & 2)
+          gv[e][j] = buf_frag<T>(rg, row_off(ov[e], nx, K, K));
+        else
           gv[e][j] = buf_frag_elems<T>(rg, ov[e] >= 0 ? uint32_t(int64_t(ov[e]) * K * ES) : kOob,
                                        nx, K);
-        }
       }
   };
   // channel-major LDS rows: both pairs' values of a channel in one write
@@ -699,16 +702,20 @@ int sp_conv_wgrad(const void* x, int64_t n_in, const void* g, int64_t n_out, int
     return set_error(SP_ERR_UNSUPPORTED, "wgrad: features exceed 4 GiB");
   // 16-byte row gathers need whole vectors per row and aligned bases
   const int v = vec_of(dtype);
-  const bool vec = C % v == 0 && K % v == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
-                   reinterpret_cast<uintptr_t>(g) % 16 == 0;
+  const int vec = (C % v == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 ? 1 : 0) |
+                  (K % v == 0 && reinterpret_cast<uintptr_t>(g) % 16 == 0 ? 2 : 0);
   const int bw = wgrad_block(C, K);
   dim3 grid(unsigned(gx), unsigned(cdiv(C, bw)), unsigned(cdiv(K, bw)));
   const int64_t tot = K * kv * C;
   const unsigned rb = unsigned(cdiv(tot, 256));
   auto run = [&](auto tag) {
     using T = decltype(tag);
-    auto kern = bw == 128 ? (vec ? wgrad_partial<T, true, 128> : wgrad_partial<T, false, 128>)
-                          : (vec ? wgrad_partial<T, true, 64> : wgrad_partial<T, false, 64>);
+    using Kern = decltype(&wgrad_partial<T, 3, 64>);
+    const Kern k64[4] = {wgrad_partial<T, 0, 64>, wgrad_partial<T, 1, 64>,
+                         wgrad_partial<T, 2, 64>, wgrad_partial<T, 3, 64>};
+    const Kern k128[4] = {wgrad_partial<T, 0, 128>, wgrad_partial<T, 1, 128>,
+                          wgrad_partial<T, 2, 128>, wgrad_partial<T, 3, 128>};
+    const Kern kern = bw == 128 ? k128[vec] : k64[vec];
     kern<<<grid, 256, 0, s>>>(static_cast<const T*>(x), n_in, static_cast<const T*>(g), n_out,
                               int(C), int(K), int(kv), in_rows, out_rows, counts, row_stride,
                               splits, part, uint32_t(xb), uint32_t(gb));

@@ -183,9 +183,10 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int):
     table's statistics back (a stream synchronization) and, when they pass,
     sorts the masks, permutes the table and reads the permuted table's
     statistics (a second one).  The outcome is memoised on the table tensor
-    (like its plan) and recomputed if the table changes.  Calls made while
-    the stream is being captured into a graph use a settled order but never
-    advance the decision."""
+    (like its plan) and recomputed if the table changes; a reordered table
+    keeps the order (M int32), a permuted copy of itself (kv * M int32) and
+    that copy's plan.  Calls made while the stream is being captured into a
+    graph use a settled order but never advance the decision."""
     mode = ROW_ORDER
     if mode == "natural":
         return None
@@ -207,8 +208,10 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int):
         pairs._spconv_triton_order = (stamp, "seen")
         return None
 
+    planned = USE_GATHER_PLAN and kv <= _PLAN_MAX_KV
+
     def mfma_rows(stats):  # rows the GEMM multiplies: per live tile or wave offset
-        return 256 * stats[1] if kv <= _PLAN_MAX_KV else 64 * stats[2]
+        return 256 * stats[1] if planned else 64 * stats[2]
 
     variant = None
     natural = table_stats(pairs, n_src) if mode == "auto" else None
@@ -217,7 +220,7 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int):
         order = mask_order(pairs)
         perm = permute_table(pairs, order)
         if mode == "mask" or mfma_rows(table_stats(perm, n_src)) <= ORDER_MAX_WORK_RATIO * done:
-            plan = gather_plan(perm, n_src) if USE_GATHER_PLAN else None
+            plan = gather_plan(perm, n_src) if planned else None
             variant = (order, perm, plan)
     pairs._spconv_triton_order = (stamp, variant if variant is not None else "natural")
     return variant

@@ -78,6 +78,7 @@ CASES = [
     (128, 256, 2500, True, 1),
     (256, 136, 3000, False, 2),
     (130, 128, 2000, True, 1),  # rows not a whole number of 16-byte vectors
+    (32, 20, 2500, True, 1),  # input rows vectors, gradient rows not
 ]
 
 
@@ -122,7 +123,7 @@ def test_forward_output_dtype(out_dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("ci", [0, 1, 3, 5, 6, 8, 9, 10])
+@pytest.mark.parametrize("ci", [0, 1, 3, 5, 6, 8, 9, 10, 11])
 def test_dgrad_and_wgrad_match_oracle(ci, dtype):
     from spconv_triton.pytorch._impl import gemm
 
