@@ -17,6 +17,8 @@
 //    batch-major order (torch.unique, pairs.py:206-219) -- a radix sort of the
 //    deduplicated keys restores that order, and the sorted position of each key
 //    is written back into its hash slot as its output row.
+#include <type_traits>
+
 #include "sp_common.h"
 #include "sp_hash.h"
 #include "sp_sort.h"
@@ -120,28 +122,36 @@ __device__ __forceinline__ Coord load_coord(const int32_t* __restrict__ idx, int
 
 // Candidate output key for (offset odometer `off`, input coordinate c)
 // following pair_kernels.py:76-91; returns false when geometrically invalid.
+// I = int32_t when every key and coordinate fits in 31 bits (int32 keys):
+// the stride division is then a 32-bit one, several times cheaper than the
+// 64-bit routine.
+template <typename I = int64_t>
 __device__ __forceinline__ bool candidate_key(const GeomDev& g, const Coord& c, const int* off,
                                               uint64_t* key) {
-  int64_t acc = c.b;
+  using U = std::make_unsigned_t<I>;
+  U acc = U(c.b);  // unsigned: wraps (defined) for invalid candidates
   bool ok = c.ok;
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
     if (d < g.ndim) {
-      const int64_t koff = int64_t(off[d]) * g.dil[d];
-      int64_t o;
+      const I koff = I(off[d]) * I(g.dil[d]);
+      const I x = I(c.x[d]);
+      I o;
       if (g.mode == SP_PAIR_TRANSPOSE) {
-        o = c.x[d] * g.st[d] - g.pad[d] + koff;
+        o = x * I(g.st[d]) - I(g.pad[d]) + koff;
       } else {
-        const int64_t num = c.x[d] + g.pad[d] - koff;
+        const I num = x + I(g.pad[d]) - koff;
         if (g.st[d] == 1) {
           o = num;
         } else {
-          ok = ok && num >= 0 && (num % g.st[d]) == 0;
-          o = num >= 0 ? num / g.st[d] : -1;
+          const U st = U(g.st[d]);
+          const U q = U(num >= 0 ? num : 0) / st;
+          ok = ok && num >= 0 && U(num) == q * st;
+          o = num >= 0 ? I(q) : I(-1);
         }
       }
-      ok = ok && o >= 0 && o < g.out_shape[d];
-      acc = acc * g.out_shape[d] + o;
+      ok = ok && o >= 0 && o < I(g.out_shape[d]);
+      acc = acc * U(g.out_shape[d]) + U(o);
     }
   }
   *key = uint64_t(acc);
@@ -165,6 +175,10 @@ __device__ __forceinline__ bool subm_source_key(const GeomDev& g, const Coord& c
   *key = uint64_t(acc);
   return ok;
 }
+
+// Integer type of a table's keys: Table32 holds keys below 2^31.
+template <class Table>
+using KeyInt = std::conditional_t<std::is_same_v<Table, Table32>, int32_t, int64_t>;
 
 __device__ __forceinline__ void odometer_next(const GeomDev& g, int* off) {
   for (int d = g.ndim - 1; d >= 0; --d) {
@@ -401,7 +415,7 @@ __global__ __launch_bounds__(256) void conv_mark(const int32_t* __restrict__ idx
   uint32_t cw = 0, cb = 0;  // pending word and its bits (cb == 0: none)
   for (int k = 0; k < g.kv; ++k) {
     uint64_t key;
-    if (candidate_key(g, c, off, &key)) {
+    if (candidate_key<int32_t>(g, c, off, &key)) {
       const uint32_t w = uint32_t(key >> 5), b = 1u << uint32_t(key & 31u);
       if (cb != 0 && w != cw) {
         atomicOr(&bits[cw], cb);
@@ -442,7 +456,7 @@ __global__ __launch_bounds__(256) void conv_fill_bitmap(
   for (int k = 0; k < g.kv; ++k) {
     uint64_t key;
     int32_t r = -1;
-    if (candidate_key(g, c, off, &key)) {
+    if (candidate_key<int32_t>(g, c, off, &key)) {
       const int64_t rank = bitmap_rank(bits, prefix, key);
       r = rank < n_keep ? int32_t(rank) : -1;
     }
@@ -472,12 +486,13 @@ __global__ __launch_bounds__(256) void emit_bitmap_keys(const uint32_t* __restri
   while (m != 0 && r < n_keep) {
     const int b = __ffs(m) - 1;
     m &= m - 1u;
-    uint64_t rem = uint64_t(w) * 32u + uint64_t(b);
+    uint32_t rem = uint32_t(w) * 32u + uint32_t(b);  // bitmap keys are below 2^31
     int32_t* o = out + r * (g.ndim + 1);
     for (int d = g.ndim - 1; d >= 0; --d) {
-      const uint64_t sd = uint64_t(g.out_shape[d]);
-      o[d + 1] = int32_t(rem % sd);
-      rem /= sd;
+      const uint32_t sd = uint32_t(g.out_shape[d]);
+      const uint32_t q = rem / sd;
+      o[d + 1] = int32_t(rem - q * sd);
+      rem = q;
     }
     o[0] = int32_t(rem);
     ++r;
@@ -518,7 +533,7 @@ __global__ __launch_bounds__(256) void conv_insert(const int32_t* __restrict__ i
   for (int k = 0; k < g.kv; ++k) {
     uint64_t key = 0;
     bool fresh = false;
-    if (live && candidate_key(g, c, off, &key)) fresh = t.insert(key, 0);
+    if (live && candidate_key<KeyInt<Table>>(g, c, off, &key)) fresh = t.insert(key, 0);
     // wave-aggregated append of newly inserted keys
     const uint64_t b = __ballot(fresh);
     if (b) {
@@ -579,7 +594,7 @@ __global__ __launch_bounds__(256) void conv_fill(const int32_t* __restrict__ idx
   for (int k = 0; k < g.kv; ++k) {
     uint64_t key;
     int32_t r = -1;
-    if (candidate_key(g, c, off, &key)) {
+    if (candidate_key<KeyInt<Table>>(g, c, off, &key)) {
       r = t.find(key);
       if (r >= n_keep) r = -1;
     }
