@@ -6,9 +6,9 @@
 // 8 or 9 bits, and for these sizes (10^5 - 10^6 items) its cost is mostly
 // latency, so fewer passes is what pays.
 //
-// Tile layout: a workgroup of 256 threads (4 waves) owns a tile of 2048
-// consecutive items, visited in 8 rounds; in round r wave w holds items
-// [r*256 + w*64, +64).  The 32 (round, wave) segments are in item order, so a
+// Tile layout: a workgroup of 512 threads (8 waves) owns a tile of 2048
+// consecutive items, visited in 4 rounds; in round r wave w holds items
+// [r*512 + w*64, +64).  The 32 (round, wave) segments are in item order, so a
 // per-digit exclusive scan over them plus the in-wave peer rank gives a stable
 // local rank.  Global placement of digit d of tile b: all items with a smaller
 // digit plus the items of digit d in tiles before b.  Up to kRsFusedTiles
@@ -21,12 +21,13 @@
 
 namespace sp {
 
-constexpr int kRsThreads = 256;
-constexpr int kRsRounds = 8;
+constexpr int kRsThreads = 512;
+constexpr int kRsRounds = 4;
+constexpr int kRsWaves = kRsThreads / 64;
 constexpr int kRsTile = kRsThreads * kRsRounds;  // 2048
 constexpr int kRsMaxBits = 9;
 constexpr int kRsMaxRadix = 1 << kRsMaxBits;             // 512
-constexpr int kRsSegs = kRsRounds * (kRsThreads / 64);  // 32
+constexpr int kRsSegs = kRsRounds * kRsWaves;  // 32: segment r * kRsWaves + wave
 constexpr int64_t kRsFusedTiles = 128;
 static_assert(kRsTile < 65536, "segment counts are stored as uint16");
 
@@ -198,7 +199,7 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter(const Item* __restrict_
     const uint64_t peers = match_digit(d, __ballot(valid), db);
     const uint64_t below = peers & lanemask_lt();
     ranks[r] = uint32_t(__popcll(below));
-    if (valid && below == 0) seg[r * 4 + wave][d] = uint16_t(__popcll(peers));
+    if (valid && below == 0) seg[r * kRsWaves + wave][d] = uint16_t(__popcll(peers));
   }
   __syncthreads();
   // per digit, exclusive scan over the 32 segments (all 32 reads in flight)
@@ -219,7 +220,8 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter(const Item* __restrict_
     const int64_t idx = base + r * kRsThreads + wave * 64 + lane;
     if (idx < n) {
       const uint32_t d = digits[r];
-      out[tile_base[d] + seg[r * 4 + wave][d] + ranks[r]] = items[r];
+      const uint32_t pos = tile_base[d] + seg[r * kRsWaves + wave][d] + ranks[r];
+      if (pos < uint64_t(n)) out[pos] = items[r];  // always true for consistent counts
     }
   }
 }
