@@ -379,3 +379,52 @@ def test_row_order_decision_waits_out_graph_capture():
     settled = gemm.conv_forward(x, w, pf, n)
     assert isinstance(pf._spconv_triton_order[1], tuple), "the next eager call settles"
     assert torch.equal(settled, eager)
+
+
+@pytest.mark.parametrize("case", ["wide_1024", "subm4d"])
+def test_mask_row_order_full_size(case):
+    """The stress configurations at their stated sizes: SubMConv3d 256 -> 256 on
+    a 400k-voxel 1024^3 surface cloud (staged kernel, overflow tiles in mask
+    order) and SubMConv4d 3^4 128 -> 128 at ~500k voxels (kv = 81: direct
+    kernel).  The mask-ordered forward equals the natural one bit for bit, and
+    the automatic rule picks the mask order for both."""
+    from bench_data import surface_cloud
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+    from spconv_triton.pytorch._impl import gemm
+
+    if case == "wide_1024":
+        idx = surface_cloud(400000, 1024, seed=0)
+        shape, ks, C = [1024] * 3, [3] * 3, 256
+    else:
+        rng = np.random.default_rng(0)
+        base = surface_cloud(8000, 512, seed=3)[:, 1:].astype(np.int64)
+        rows = []
+        for t in range(64):
+            c = np.clip(base + (np.array([t // 8, t // 16, t // 4]) % 512), 0, 511)
+            c = c[rng.random(c.shape[0]) < 0.98]
+            rows.append(np.concatenate([np.zeros((c.shape[0], 1), np.int64),
+                                        np.full((c.shape[0], 1), t), c], 1))
+        idx = np.unique(np.concatenate(rows).astype(np.int32), axis=0)
+        shape, ks, C = [64, 512, 512, 512], [3] * 4, 128
+    nd = len(shape)
+    res = ops.get_indice_pairs_implicit_gemm(torch.from_numpy(idx).to(DEV), 1, shape,
+                                             ConvAlgo.MaskImplicitGemm, ks, [1] * nd, [1] * nd,
+                                             [1] * nd, [0] * nd, True, False, is_train=False)
+    pf = res[2]
+    n = idx.shape[0]
+    kv = pf.shape[0]
+    torch.manual_seed(1)
+    x = torch.randn(n, C, device=DEV).half()
+    w = (torch.randn(C, kv, C, device=DEV) / np.sqrt(kv * C)).half()
+    outs = {}
+    for mode in ("natural", "mask"):
+        gemm.ROW_ORDER = mode
+        try:
+            outs[mode] = gemm.conv_forward(x, w, pf, n)
+        finally:
+            gemm.ROW_ORDER = "auto"
+    assert torch.equal(outs["natural"], outs["mask"])
+    pf2 = pf.clone()  # a fresh table: the automatic rule decides at its second wide call
+    assert gemm.row_order_variant(pf2, n, C * C) is None
+    assert gemm.row_order_variant(pf2, n, C * C) is not None
