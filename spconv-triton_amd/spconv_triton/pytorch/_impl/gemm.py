@@ -91,9 +91,23 @@ def packed_weight(filters: torch.Tensor, bias: torch.Tensor | None, dtype: torch
 
 
 #: Use gather plans (per-tile distinct source rows staged in LDS) for the
-#: forward and input-gradient GEMMs.  Results are bit-identical either way;
-#: tests switch this off to compare the two kernels' modes.
-USE_GATHER_PLAN = True
+#: forward and input-gradient GEMMs: True (always), False (never) or "auto":
+#: when rows * max(C, K) >= PLAN_MIN_WORK.  A plan costs a build per table
+#: (~25 us, more on large tables) and pays back per GEMM in proportion to the
+#: GEMM's size: measured, plans slow a LiDAR encoder whose tables are <= 80k
+#: rows of <= 64 channels (1.72 -> 1.78 ms per pass) and speed up the ResUNet
+#: training step (88k - 240k rows, up to 256 channels; 10.75 -> 10.60 ms) and
+#: the 200k-row 64-channel metric layer (direct kernel ~1.6x slower).
+#: Results are bit-identical either way; tests force True / False to compare
+#: the two kernels.
+USE_GATHER_PLAN = "auto"
+PLAN_MIN_WORK = 100_000 * 64
+
+
+def _use_plan(M: int, C: int, K: int) -> bool:
+    if USE_GATHER_PLAN == "auto":
+        return M * max(C, K) >= PLAN_MIN_WORK
+    return bool(USE_GATHER_PLAN)
 
 
 def gather_plan(pairs: torch.Tensor, n_src: int):
@@ -101,12 +115,15 @@ def gather_plan(pairs: torch.Tensor, n_src: int):
     when kv is outside the planned kernel's range.  Memoised on the table
     tensor, like the reference memoises its tables on the indice data
     (pairs.py:429-469); rebuilt if the table is modified in place.  The build
-    is asynchronous (no host synchronization)."""
+    is asynchronous (no host synchronization).  None as well while the stream
+    is being captured and no plan is cached (the GEMM then gathers directly)."""
     kv, M = pairs.shape
     cached = getattr(pairs, "_spconv_triton_plan", None)
     stamp = (int(n_src), pairs._version, pairs.data_ptr())
     if cached is not None and cached[0] == stamp:
         return cached[1]
+    if torch.cuda.is_current_stream_capturing():
+        return None  # a build captured into a graph would rerun on every replay
     L = _lib.lib()
     nbytes = L.sp_gather_plan_bytes(M, kv)
     if nbytes == 0:
@@ -172,10 +189,10 @@ def permute_table(pairs: torch.Tensor, order: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def row_order_variant(pairs: torch.Tensor, n_src: int, work: int):
+def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool = True):
     """(order, permuted table, its gather plan or None) when a GEMM of
     ``work`` = C * K on this table should take its rows in mask order (see
-    ROW_ORDER), else None.
+    ROW_ORDER), else None.  ``plan_ok``: the call may use a gather plan.
 
     In auto mode only tables that wide layers use more than once are looked
     at: the first wide call on a table runs in natural order and launches
@@ -208,7 +225,7 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int):
         pairs._spconv_triton_order = (stamp, "seen")
         return None
 
-    planned = USE_GATHER_PLAN and kv <= _PLAN_MAX_KV
+    planned = plan_ok and kv <= _PLAN_MAX_KV
 
     def mfma_rows(stats):  # rows the GEMM multiplies: per live tile or wave offset
         return 256 * stats[1] if planned else 64 * stats[2]
@@ -238,7 +255,8 @@ def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: 
     kv = pairs.shape[0]
     packed = packed_weight(filters, bias, a.dtype, transpose)
     L = _lib.lib()
-    variant = row_order_variant(pairs, a.shape[0], K * C)
+    use_plan = _use_plan(M, C, K)
+    variant = row_order_variant(pairs, a.shape[0], K * C, use_plan)
     if variant is not None:
         order, perm, plan = variant
         _lib.check(L.sp_conv_gemm_ordered(
@@ -247,7 +265,7 @@ def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: 
             _lib.ptr(plan), 0 if plan is None else plan.numel(), _lib.ptr(out),
             _lib.dtype_code(out.dtype), _lib.stream_of(a.device)), "sp_conv_gemm_ordered")
         return
-    plan = gather_plan(pairs, a.shape[0]) if USE_GATHER_PLAN else None
+    plan = gather_plan(pairs, a.shape[0]) if use_plan else None
     if plan is not None:
         # the planned kernel skips empty offsets itself: mask tables are not needed
         _lib.check(L.sp_conv_gemm_planned(
