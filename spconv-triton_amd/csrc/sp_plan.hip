@@ -101,12 +101,21 @@ __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
     const int nw = int((window + 31) / 32);
     for (int w = tid; w < nw; w += kPlanThreads) bm[w] = 0u;
     __syncthreads();
+    // a thread's entries are one row's neighbours, often in the same word:
+    // bits of consecutive entries in one word go out as one atomic
+    uint32_t pw = 0xffffffffu, pbits = 0u;
 #pragma unroll
     for (int i = 0; i < PER; ++i)
       if (v[i] != kNone) {
         const uint32_t d = uint32_t(v[i] - lo);
-        atomicOr(&bm[d >> 5], 1u << (d & 31));
+        if ((d >> 5) != pw) {
+          if (pbits) atomicOr(&bm[pw], pbits);
+          pw = d >> 5;
+          pbits = 0u;
+        }
+        pbits |= 1u << (d & 31);
       }
+    if (pbits) atomicOr(&bm[pw], pbits);
     __syncthreads();
     // thread t ranks words [t * wpt, (t + 1) * wpt)
     const int wpt = (nw + kPlanThreads - 1) / kPlanThreads;
