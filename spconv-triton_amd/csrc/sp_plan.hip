@@ -186,18 +186,24 @@ __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
   // it without waiting for the count
   for (int i = U + tid; i < kLdsRows; i += kPlanThreads) rows_t[i] = -1;
 
-  // items of the tile: the offsets with a pair among its rows
-  if (tid == 0) {
+  // items of the tile: the offsets with a pair among its rows, numbered in
+  // ascending order by one wave (kv <= kPlanMaxKv = 64 lanes)
+  static_assert(kPlanMaxKv <= 64, "one wave numbers the items");
+  if (tid < 64) {
     int32_t* ko = koff_out + tile * E;
-    int n = 0;
-    for (int k = 0; k < kv; ++k)
-      if (s_item[k] == 0) {
-        s_item[k] = n;
-        ko[n++] = k;
-      }
-    for (int q = n; q < E; ++q) ko[q] = -1;
-    s_nact = n;
-    nact_out[tile] = n;
+    const bool live = tid < kv && s_item[tid] == 0;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(live);
+    const int n = __popcll(m);
+    if (live) {
+      const int item = __popcll(m & ((uint64_t(1) << tid) - 1));
+      s_item[tid] = item;
+      ko[item] = tid;
+    }
+    if (tid >= n && tid < E) ko[tid] = -1;
+    if (tid == 0) {
+      s_nact = n;
+      nact_out[tile] = n;
+    }
   }
   __syncthreads();
   // LDS address of every (item, row): the staged slot of the row's rank, or
