@@ -428,3 +428,23 @@ def test_mask_row_order_full_size(case):
     pf2 = pf.clone()  # a fresh table: the automatic rule decides at its second wide call
     assert gemm.row_order_variant(pf2, n, C * C) is None
     assert gemm.row_order_variant(pf2, n, C * C) is not None
+
+
+@pytest.mark.parametrize("M", [1, 63, 255, 257, 1000])
+def test_mask_row_order_partial_tiles(M):
+    """Ordered GEMM on tables whose last tile is partial (rows past M must not
+    be written through the order) and on a single row, staged and direct."""
+    from spconv_triton.pytorch._impl import gemm
+
+    rng = np.random.default_rng(M)
+    kv, n_src, C, K = 27, 700, 40, 72
+    t = rng.integers(0, n_src, size=(kv, M)).astype(np.int32)
+    t[rng.random((kv, M)) > 0.3] = -1
+    pf = torch.from_numpy(t).to(DEV)
+    torch.manual_seed(M)
+    x, _ = _q(torch.randn(n_src, C), torch.float16)
+    w, _ = _q(torch.randn(K, kv, C) * 0.05, torch.float16)
+    outs = _orders(x, w, None, False, pf, M)
+    ref = outs[("natural", True)]
+    for key, o in outs.items():
+        assert torch.equal(o, ref), f"{key} differs from the natural planned GEMM"
