@@ -460,3 +460,27 @@ def test_module_rulebooks_defer_mask_sorts(training):
         exp = orc.igemm_pairs(ind, 2, shape_k, ks, st, pad, dil, op, subm, tr, is_train)
         res = (data.out_indices, exp[1], data.pair_fwd, data.pair_bwd) + splits + (data.masks,)
         _compare_igemm(res, exp, data.indices if subm else None, subm, is_train)
+
+
+def test_deferred_mask_splits_deepcopy():
+    """A deep copy of a module-built rulebook (e.g. of a SparseConvTensor's
+    indice_dict) carries the computed mask splits."""
+    import copy
+
+    import spconv_triton.pytorch as spconv
+
+    rng = np.random.default_rng(5)
+    shape = [20, 18, 16]
+    idx = rand_indices(rng, 1, shape, 900)
+    conv = spconv.SparseConv3d(4, 8, 3, stride=2, padding=1, indice_key="c").to(DEV)
+    x = spconv.SparseConvTensor(torch.randn(idx.shape[0], 4, device=DEV),
+                                torch.from_numpy(idx).to(DEV), shape, 1)
+    y = conv(x)
+    data = y.indice_dict["c"]
+    dup = copy.deepcopy(data)
+    for name in ("pair_mask_fwd_splits", "pair_mask_bwd_splits", "mask_argsort_fwd_splits",
+                 "mask_argsort_bwd_splits"):
+        a, b = getattr(data, name), getattr(dup, name)
+        assert len(a) == len(b) > 0, name
+        for u, v in zip(a, b):
+            assert torch.equal(u, v) and u.data_ptr() != v.data_ptr(), name
