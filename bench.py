@@ -83,33 +83,71 @@ def plan_read_bytes(plan, kv: int, n_out: int) -> int:
     return int((count[staged] * 4).sum() + (items[staged] * tile * 2).sum())
 
 
+def _time_reps(fn, budget_s, max_reps):
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or reps >= max_reps:
+            return el / reps, reps
+
+
 def cpu_baseline(idx, feats_np, w_np, b_np, pf_np):
-    """Oracle forward (fp32) on a bounded row sample; returns the dict for the JSON line."""
+    """Oracle forward (fp32) on bounded row samples; returns the dict for the JSON line.
+
+    * value: all allowed host threads, 50k of the 200k output rows;
+    * single_thread: one thread, 5k rows;
+    * config1: BASELINE config 1 in full (2,000 uniform voxels in 64^3,
+      SubMConv3d 16 -> 16 fp32): the oracle's sort-based rulebook plus its
+      forward, at all threads and at one thread."""
     import numpy as np
 
+    from bench_data import uniform_cloud
     from oracle import oracle as orc
 
     threads = len(os.sched_getaffinity(0))
     threads = min(threads, int(os.environ.get("OMP_NUM_THREADS", threads)))
+    w = w_np.reshape(C_OUT, KV, C_IN).astype(np.float32)
+    x = feats_np.astype(np.float32)
+    b = b_np.astype(np.float32)
+
     orc.set_num_threads(threads)
     rows = 50_000
     pf_s = np.ascontiguousarray(pf_np[:, :rows])
-    w = w_np.reshape(C_OUT, KV, C_IN).astype(np.float32)
-    x = feats_np.astype(np.float32)
-    reps = 0
-    t0 = time.perf_counter()
-    while True:
-        orc.gemm_fwd_f32(x, w, pf_s, b_np.astype(np.float32))
-        reps += 1
-        el = time.perf_counter() - t0
-        if el > 10.0 or reps >= 50:
-            break
-    per_row = el / (reps * rows)
+    per_pass, reps = _time_reps(lambda: orc.gemm_fwd_f32(x, w, pf_s, b), 10.0, 50)
+    per_row = per_pass / rows
     # the reference's pair generation on the CPU (sort + binary search) for the full cloud
     t1 = time.perf_counter()
     orc.igemm_pairs(idx, 1, [GRID] * 3, [3] * 3, [1] * 3, [1] * 3, [1] * 3, [0] * 3, True, False,
                     False)
     pairgen_s = time.perf_counter() - t1
+
+    orc.set_num_threads(1)
+    rows1 = 5_000
+    pf_1 = np.ascontiguousarray(pf_np[:, :rows1])
+    per_pass1, reps1 = _time_reps(lambda: orc.gemm_fwd_f32(x, w, pf_1, b), 4.0, 50)
+    per_row1 = per_pass1 / rows1
+
+    # BASELINE config 1: 2,000 uniform voxels in 64^3, SubMConv3d 16 -> 16 fp32, batch 1
+    idx1 = uniform_cloud(2000, [64] * 3, seed=0)
+    rng = np.random.default_rng(0)
+    x1 = rng.standard_normal((idx1.shape[0], 16)).astype(np.float32)
+    bound = 1.0 / np.sqrt(16 * 27)
+    w1 = rng.uniform(-bound, bound, (16, 27, 16)).astype(np.float32)
+    b1 = rng.uniform(-bound, bound, 16).astype(np.float32)
+
+    def config1():
+        res = orc.igemm_pairs(idx1, 1, [64] * 3, [3] * 3, [1] * 3, [1] * 3, [1] * 3, [0] * 3,
+                              True, False, False)
+        orc.gemm_fwd_f32(x1, w1, res[2], b1)
+
+    c1 = {}
+    for nt in (threads, 1):
+        orc.set_num_threads(nt)
+        c1[nt] = _time_reps(config1, 2.0, 200)[0]
+    orc.set_num_threads(threads)
     return {
         "value": round(1.0 / per_row / 1e6, 4),
         "unit": "Mvoxels/s",
@@ -120,6 +158,12 @@ def cpu_baseline(idx, feats_np, w_np, b_np, pf_np):
                    f"threads; oracle sort-based pair generation of the full cloud "
                    f"{pairgen_s * 1e3:.1f} ms"),
         "pairgen_ms": round(pairgen_s * 1e3, 2),
+        "single_thread": {"value": round(1.0 / per_row1 / 1e6, 4), "unit": "Mvoxels/s",
+                          "cores": 1, "sample": f"{rows1} output rows x {reps1} passes"},
+        "config1": {"workload": "SubMConv3d k3 16->16 fp32, 2000 uniform voxels in 64^3, "
+                                "batch 1: oracle rulebook + forward",
+                    "ms": round(c1[threads] * 1e3, 3), "cores": threads,
+                    "ms_1thread": round(c1[1] * 1e3, 3)},
     }
 
 
@@ -156,6 +200,7 @@ def main() -> int:
     from bench_data import surface_cloud
     from spconv_triton.core import ConvAlgo
     from spconv_triton.pytorch import ops
+    from spconv_triton.pytorch._impl import _lib
     from spconv_triton.pytorch._impl import gemm as gemm_impl
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -235,30 +280,60 @@ def main() -> int:
         wall_s = time.perf_counter() - t0
         ms_per_step = wall_s / args.steps * 1e3
 
-        # kernel-level timing for the roofline: events on the stream the GEMM
-        # kernel runs on (torch's current stream, which the library uses)
-        stream = torch.cuda.current_stream()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 500
-        s.record(stream)
-        for _ in range(reps):
-            graph.replay()
-        e.record(stream)
-        torch.cuda.synchronize()
-        kernel_ms = s.elapsed_time(e) / reps
+    # ---- the GEMM kernel alone, for the roofline: one graph holding
+    # GEMM_LAUNCHES back-to-back launches of the planned gather-GEMM (the
+    # module's graph above also holds the weight pack), replayed between HIP
+    # events on the stream the launches are captured on
+    pf_c = y0.indice_dict["subm0"].pair_fwd
+    plan = gemm_impl.gather_plan(pf_c, N_VOXELS)
+    packed = gemm_impl.packed_weight(conv.weight, conv.bias, torch.float16, False)
+    out_k = torch.empty((N_VOXELS, C_OUT), dtype=torch.float16, device=dev)
+    L = _lib.lib()
+    f16 = _lib.dtype_code(torch.float16)
+    kstream = torch.cuda.Stream()
+    kstream.wait_stream(torch.cuda.current_stream())
+
+    def launch():
+        _lib.check(L.sp_conv_gemm_planned(_lib.ptr(feats), f16, N_VOXELS, _lib.ptr(packed), C_OUT,
+                                          KV, C_IN, 0, 1, _lib.ptr(pf_c), N_VOXELS,
+                                          _lib.ptr(plan), plan.numel(), _lib.ptr(out_k), f16,
+                                          _lib.stream_of(dev)), "sp_conv_gemm_planned")
+
+    GEMM_LAUNCHES = 20
+    with torch.cuda.stream(kstream):
+        launch()
+        kgraph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(kgraph, stream=kstream):
+            for _ in range(GEMM_LAUNCHES):
+                launch()
+        kgraph.replay()
+        kstream.synchronize()
+        if not torch.equal(out_k, y.features):
+            raise RuntimeError("the kernel graph differs from the module forward")
+        ks, ke = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        replays = 25
+        ks.record(kstream)
+        for _ in range(replays):
+            kgraph.replay()
+        ke.record(kstream)
+        kstream.synchronize()
+    kernel_ms = ks.elapsed_time(ke) / (replays * GEMM_LAUNCHES)
 
     # HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE runs,
-    # scaled by a 256 MiB copy (profiles/gather_gemm_traffic.json)
+    # scaled by a 256 MiB copy: a stored profile, not measured in this run
     traffic = None
     tfile = ROOT / "profiles" / "gather_gemm_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("bytes_per_launch")
-    plan = gemm_impl.gather_plan(y0.indice_dict["subm0"].pair_fwd, N_VOXELS)
     n_overflow = gemm_impl.plan_overflow_count(plan)
     nbytes = gemm_bytes(N_VOXELS, N_VOXELS, plan_read_bytes(plan, KV, N_VOXELS))
     flops = 2.0 * n_pairs * C_IN * C_OUT
     achieved = nbytes / (kernel_ms * 1e-3) / 1e9
     mvox = N_VOXELS / (ms_per_step * 1e-3) / 1e6
+    # pair generation (subm, eval): coordinates read, pair_fwd written, sorted
+    # mask words + argsort written
+    pg_bytes = 4 * N_VOXELS * 4 + 4 * KV * N_VOXELS + 8 * N_VOXELS
+    pg_achieved = pg_bytes / (rules_ms * 1e-3) / 1e9
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -300,11 +375,26 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "traffic_source": "stored rocprofv3 FETCH_SIZE/WRITE_SIZE profile "
+                              "(profiles/gather_gemm_traffic.json), not this run",
             "kernel": "gather_gemm_staged<f16,f16,VEC>",
             "kernel_ms": round(kernel_ms, 5),
+            "kernel_ms_source": f"HIP events around {GEMM_LAUNCHES}-launch graphs of the GEMM "
+                                "alone, per launch",
             "algorithmic_bytes": nbytes,
             "mfma_tflops": round(flops / (kernel_ms * 1e-3) / 1e12, 2),
             "mfma_frac": round(flops / (kernel_ms * 1e-3) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+        },
+        "pairgen_roofline": {
+            "bound": "hbm",
+            "achieved": round(pg_achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(pg_achieved / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": pg_bytes,
+            "ms": round(rules_ms, 5),
+            "what": "cold subm rulebook (eval): 4*N*(D+1) coordinates + 4*kv*N pair_fwd + "
+                    "8*N sorted mask words and argsort, over the rulebook's time",
         },
         "cpu_baseline": cpu,
     }

@@ -106,51 +106,29 @@ __global__ __launch_bounds__(kRsThreads) void rs_hist(const Item* __restrict__ i
 }
 
 // Placement of this tile's digits from tile-major histograms, into
-// tile_base[0..R).  Thread t owns digits [t * P, t * P + P), P = R / 256 or 1,
-// read as one contiguous P-word vector per tile (a wave reads 256 or 512
-// consecutive bytes of a histogram row); 32 tiles per memory round trip.
+// tile_base[0..R).  Thread t owns digit t (R <= kRsMaxRadix == kRsThreads), so
+// a wave reads 256 consecutive bytes of a histogram row; 64 tiles per memory
+// round trip.
+static_assert(kRsMaxRadix <= kRsThreads, "one digit per thread in fused_tile_base");
 __device__ __forceinline__ void fused_tile_base(const uint32_t* __restrict__ hist, int64_t ntiles,
                                                 int R, uint32_t* tile_base, uint32_t* scan_lds) {
-  constexpr int kBatch = 32;
+  constexpr int kBatch = 64;
   const int64_t me = blockIdx.x;
-  uint32_t tot0 = 0, tot1 = 0, pre0 = 0, pre1 = 0;
-  if (R > kRsThreads) {  // two digits per thread
-    const int d0 = int(threadIdx.x) * 2;
-    for (int64_t b = 0; b < ntiles; b += kBatch) {
-      uint2 h[kBatch];
+  uint32_t tot = 0, pre = 0;
+  const int d = int(threadIdx.x);
+  for (int64_t b = 0; b < ntiles; b += kBatch) {
+    uint32_t h[kBatch];
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u)
-        h[u] = b + u < ntiles ? *reinterpret_cast<const uint2*>(hist + (b + u) * R + d0)
-                              : make_uint2(0u, 0u);
+    for (int u = 0; u < kBatch; ++u) h[u] = (b + u < ntiles && d < R) ? hist[(b + u) * R + d] : 0u;
 #pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        tot0 += h[u].x;
-        tot1 += h[u].y;
-        pre0 += b + u < me ? h[u].x : 0u;
-        pre1 += b + u < me ? h[u].y : 0u;
-      }
+    for (int u = 0; u < kBatch; ++u) {
+      tot += h[u];
+      pre += b + u < me ? h[u] : 0u;
     }
-    uint32_t all = 0;
-    const uint32_t run = block_exclusive_scan<kRsThreads>(tot0 + tot1, scan_lds, &all);
-    tile_base[d0] = run + pre0;
-    tile_base[d0 + 1] = run + tot0 + pre1;
-  } else {
-    const int d = int(threadIdx.x);
-    for (int64_t b = 0; b < ntiles; b += 2 * kBatch) {
-      uint32_t h[2 * kBatch];
-#pragma unroll
-      for (int u = 0; u < 2 * kBatch; ++u)
-        h[u] = (b + u < ntiles && d < R) ? hist[(b + u) * R + d] : 0u;
-#pragma unroll
-      for (int u = 0; u < 2 * kBatch; ++u) {
-        tot0 += h[u];
-        pre0 += b + u < me ? h[u] : 0u;
-      }
-    }
-    uint32_t all = 0;
-    const uint32_t run = block_exclusive_scan<kRsThreads>(tot0, scan_lds, &all);
-    if (d < R) tile_base[d] = run + pre0;
   }
+  uint32_t all = 0;
+  const uint32_t run = block_exclusive_scan<kRsThreads>(tot, scan_lds, &all);
+  if (d < R) tile_base[d] = run + pre;
 }
 
 template <class Item, class Digit>

@@ -69,8 +69,15 @@ _PACKED = _PackCache()
 def packed_weight(filters: torch.Tensor, bias: torch.Tensor | None, dtype: torch.dtype,
                   transpose: bool) -> torch.Tensor:
     """Weights (+ bias) relaid into the MFMA operand layout of ``dtype``; see
-    ``sp_conv_pack_weight``.  filters is KRSC [K, *ksize, C]."""
-    hit = _PACKED.get(filters, bias, dtype, transpose)
+    ``sp_conv_pack_weight``.  filters is KRSC [K, *ksize, C].
+
+    While the stream is being captured into a graph the cache is bypassed: the
+    pack kernel is captured with the GEMM, so every replay reads the weight's
+    current values (an optimizer step or ``load_state_dict`` between replays
+    updates the weight in place, which no cache stamp can see from inside a
+    replay)."""
+    capturing = torch.cuda.is_current_stream_capturing()
+    hit = None if capturing else _PACKED.get(filters, bias, dtype, transpose)
     if hit is not None:
         return hit
     K, C = filters.shape[0], filters.shape[-1]
@@ -86,7 +93,8 @@ def packed_weight(filters: torch.Tensor, bias: torch.Tensor | None, dtype: torch
     _lib.check(L.sp_conv_pack_weight(_lib.ptr(w), _lib.dtype_code(w.dtype), _lib.ptr(b), K, kv,
                                      C, dt, int(transpose), _lib.ptr(packed),
                                      _lib.stream_of(w.device)), "sp_conv_pack_weight")
-    _PACKED.put(filters, bias, dtype, transpose, packed)
+    if not capturing:
+        _PACKED.put(filters, bias, dtype, transpose, packed)
     return packed
 
 

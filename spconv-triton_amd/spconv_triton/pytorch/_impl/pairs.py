@@ -244,13 +244,14 @@ class DeferredMaskSplits:
         self._stream = torch.cuda.current_stream(pair_fwd.device)
         self._value = None
 
-    def __deepcopy__(self, memo):
-        # a copy holds the computed splits (streams and pending work do not copy)
-        import copy
-        new = DeferredMaskSplits.__new__(DeferredMaskSplits)
-        new._args, new._stream = None, None
-        new._value = copy.deepcopy(self.get(), memo)
-        return new
+    def __getstate__(self):
+        # pickles and deep copies hold the computed splits: a stream and the
+        # pending arguments are not copyable (torch.cuda.Stream does not pickle)
+        return {"_value": self.get()}
+
+    def __setstate__(self, state):
+        self._args, self._stream = None, None
+        self._value = state["_value"]
 
     def get(self):
         """(pair_mask_fwd_splits, pair_mask_bwd_splits, mask_argsort_fwd_splits,

@@ -231,3 +231,63 @@ def test_large_metric_shape_properties():
     ref = orc.gemm_fwd(xn, wn, pf[:, rows].cpu().numpy())
     out = y[rows].cpu().double().numpy()
     assert (np.abs(out - ref) <= 1e-5 * np.abs(ref) + 1e-5).all()
+
+
+# kernel volumes above one 64-offset group of the direct kernel: (shape,
+# ksize, C, K, voxels per sample, subm, stride)
+WIDE_KV = [
+    ([12, 12, 10, 10], [3, 3, 3, 3], 32, 48, 2500, True, 1),  # kv = 81, 4-D
+    ([20, 20, 20], [5, 5, 5], 24, 40, 2500, True, 1),  # kv = 125
+    ([24, 24, 24], [5, 5, 5], 16, 32, 3000, False, 2),  # kv = 125, strided
+    ([10, 10, 8, 8], [3, 3, 3, 3], 128, 128, 1200, True, 1),  # kv = 81, config 5 case 1 widths
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("ci", range(len(WIDE_KV)))
+def test_wide_kernel_volume_matches_oracle(ci, dtype):
+    """Forward, input gradient and weight gradient with kv = 81 / 125 against
+    the fp64 oracle, in natural and in mask row order (reference
+    gemm.py:254-321: every offset group, including the ones past offset 63)."""
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+    from spconv_triton.pytorch._impl import gemm
+
+    shape, ks, C, K, n, subm, stride = WIDE_KV[ci]
+    nd = len(shape)
+    rng = np.random.default_rng(300 + ci)
+    idx = rand_indices(rng, 2, shape, n)
+    pad = [k // 2 for k in ks]
+    res = ops.get_indice_pairs_implicit_gemm(torch.from_numpy(idx).to(DEV), 2, shape,
+                                             ConvAlgo.MaskImplicitGemm, ks, [stride] * nd, pad,
+                                             [1] * nd, [0] * nd, subm, False, is_train=True)
+    pf, pb = res[2], res[3]
+    kv, n_out = pf.shape
+    assert kv == int(np.prod(ks)) > 64
+    exp = orc.igemm_pairs(idx, 2, shape, ks, [stride] * nd, pad, [1] * nd, [0] * nd, subm,
+                          False, True)
+    np.testing.assert_array_equal(pf.cpu().numpy(), exp[2])
+    torch.manual_seed(400 + ci)
+    x, xn = _q(torch.randn(idx.shape[0], C), dtype)
+    g, gn = _q(torch.randn(n_out, K), dtype)
+    w, wn = _q(torch.randn(K, kv, C) / np.sqrt(kv * C), dtype)
+    b, bn = _q(torch.randn(K) * 0.1, dtype)
+    ref = orc.gemm_fwd(xn, wn, pf.cpu().numpy(), bn)
+    ref_dx = orc.gemm_dgrad(gn, wn, pb.cpu().numpy())
+    prev = gemm.ROW_ORDER
+    try:
+        for mode in ("natural", "mask"):
+            gemm.ROW_ORDER = mode
+            out = gemm.conv_forward(x, w, pf, n_out, bias=b)
+            _check(out, ref, dtype, f"forward kv={kv} ({mode} order)")
+            dx = gemm.conv_backward_input(g, w, pb, idx.shape[0])
+            _check(dx, ref_dx, dtype, f"dgrad kv={kv} ({mode} order)")
+    finally:
+        gemm.ROW_ORDER = prev
+    ref_dw = orc.gemm_wgrad(xn, gn, pf.cpu().numpy(), K, C)
+    dw = gemm.conv_backward_weight(x, g, pf, (K, kv, C))
+    scale = np.sqrt(np.maximum(1.0, orc.gemm_wgrad(np.abs(xn), np.abs(gn), pf.cpu().numpy(),
+                                                    K, C)))
+    tol = TOL[dtype](ref_dw) + 1e-6 * scale
+    err = np.abs(dw.float().cpu().double().numpy() - ref_dw)
+    assert (err <= tol).all(), f"wgrad kv={kv} max err {err.max():.3e}"

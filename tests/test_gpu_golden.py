@@ -240,3 +240,74 @@ def test_native_and_igemm_modules_agree(algo):
     b = run(algo)
     assert torch.equal(a.indices, b.indices)
     torch.testing.assert_close(a.features, b.features, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("case_id", ["tables_jointable", "tables_addtable"])
+def test_tables_golden(golden, case_id):
+    """JoinTable / AddTable over two SubMConv2d branches of one input, against
+    spconv's outputs (reference tests/test_misc_modules.py:15-33)."""
+    import spconv_triton.pytorch as spconv
+
+    case = golden("misc.pt", case_id)
+    x, _ = _sparse_input(case["input"], False)
+    branches = [build_layer(s, torch.float32) for s in case["branch_specs"]]
+    with torch.no_grad():
+        outs = [b(x) for b in branches]
+        out = getattr(spconv, case["table"])()(outs)
+    expect = case["expect"]
+    order = canonical_order(out.indices.cpu(), out.spatial_shape)
+    assert torch.equal(out.indices.cpu()[order], expect["out_indices"])
+    assert_close(out.features.cpu()[order], expect["out_features"], expect["atol_out"], case_id)
+    assert list(out.spatial_shape) == list(expect["out_spatial_shape"])
+
+
+def _keyed_input(n=600, shape=(16, 16, 16), C=8, seed=0):
+    import spconv_triton.pytorch as spconv
+
+    rng = np.random.default_rng(seed)
+    lin = rng.choice(int(np.prod(shape)), size=n, replace=False)
+    c = np.stack(np.unravel_index(lin, shape), 1)
+    idx = np.concatenate([np.zeros((n, 1)), c], 1).astype(np.int32)
+    return spconv.SparseConvTensor(torch.randn(n, C, device=DEV),
+                                   torch.from_numpy(idx).to(DEV), list(shape), 1)
+
+
+def test_indice_key_validation_errors():
+    """indice_key reuse rules (reference conv.py:211-219, :282-289, :515-567,
+    tests/test_conv_edge.py:29-45): a non-subm layer on a key that already
+    exists, a different algo on a shared key, and subm layers sharing a key
+    with a different kernel size, dilation, spatial shape or row count."""
+    import spconv_triton.pytorch as spconv
+
+    x = _keyed_input()
+    with torch.no_grad():
+        a = spconv.SubMConv3d(8, 8, 3, padding=1, indice_key="k").to(DEV)(x)
+        # a strided layer may not register a key that exists
+        with pytest.raises(AssertionError):
+            spconv.SparseConv3d(8, 8, 3, stride=2, padding=1, indice_key="k").to(DEV)(a)
+        # the layers of one key must share the algorithm
+        with pytest.raises(AssertionError, match="same algo"):
+            spconv.SubMConv3d(8, 8, 3, padding=1, indice_key="k",
+                              algo=spconv.ConvAlgo.Native).to(DEV)(a)
+        with pytest.raises(ValueError, match="same kernel"):
+            spconv.SubMConv3d(8, 8, 5, padding=2, indice_key="k",
+                              large_kernel_fast_algo=True).to(DEV)(a)
+        with pytest.raises(ValueError, match="same dilation"):
+            spconv.SubMConv3d(8, 8, 3, padding=2, dilation=2, indice_key="k").to(DEV)(a)
+        other = spconv.SparseConvTensor(a.features, a.indices, [20, 16, 16], 1,
+                                        indice_dict=a.indice_dict)
+        with pytest.raises(ValueError, match="same spatial structure"):
+            spconv.SubMConv3d(8, 8, 3, padding=1, indice_key="k").to(DEV)(other)
+        fewer = spconv.SparseConvTensor(a.features[:500], a.indices[:500], [16, 16, 16], 1,
+                                        indice_dict=a.indice_dict)
+        with pytest.raises(ValueError, match="same num of indices"):
+            spconv.SubMConv3d(8, 8, 3, padding=1, indice_key="k").to(DEV)(fewer)
+        # reuse by a matching subm layer is fine and returns the same rows
+        b = spconv.SubMConv3d(8, 8, 3, padding=1, indice_key="k").to(DEV)(a)
+        assert b.indices is a.indices
+        # an inverse layer on a key its strided layer registered must match it
+        d = spconv.SparseConv3d(8, 8, 3, stride=2, padding=1, indice_key="d").to(DEV)(b)
+        with pytest.raises(ValueError, match="same kernel"):
+            spconv.SparseInverseConv3d(8, 8, 2, indice_key="d").to(DEV)(d)
+        up = spconv.SparseInverseConv3d(8, 8, 3, indice_key="d").to(DEV)(d)
+        assert torch.equal(up.indices, b.indices)

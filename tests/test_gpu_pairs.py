@@ -484,3 +484,92 @@ def test_deferred_mask_splits_deepcopy():
         assert len(a) == len(b) > 0, name
         for u, v in zip(a, b):
             assert torch.equal(u, v) and u.data_ptr() != v.data_ptr(), name
+
+
+def test_module_rulebook_pickles():
+    """A SparseConvTensor whose indice_dict holds a module-built rulebook with
+    deferred mask sorts pickles (the sorts run first; the copy holds their
+    values), before and after the splits are read."""
+    import pickle
+
+    import spconv_triton.pytorch as spconv
+
+    rng = np.random.default_rng(6)
+    shape = [20, 18, 16]
+    idx = rand_indices(rng, 1, shape, 900)
+    conv = spconv.SparseConv3d(4, 8, 3, stride=2, padding=1, indice_key="c").to(DEV)
+    subm = spconv.SubMConv3d(8, 8, 3, padding=1, indice_key="s").to(DEV)
+    x = spconv.SparseConvTensor(torch.randn(idx.shape[0], 4, device=DEV),
+                                torch.from_numpy(idx).to(DEV), shape, 1)
+    y = subm(conv(x))
+    for key in ("c", "s"):
+        assert y.indice_dict[key]._deferred_masks is not None
+    y2 = pickle.loads(pickle.dumps(y))
+    assert torch.equal(y2.features, y.features) and torch.equal(y2.indices, y.indices)
+    for key in ("c", "s"):
+        a, b = y.indice_dict[key], y2.indice_dict[key]
+        assert torch.equal(a.pair_fwd, b.pair_fwd)
+        for name in ("pair_mask_fwd_splits", "mask_argsort_fwd_splits"):
+            u, v = getattr(a, name), getattr(b, name)
+            assert len(u) == len(v) > 0
+            for s, t in zip(u, v):
+                assert torch.equal(s, t), (key, name)
+
+
+@pytest.mark.parametrize("subm,big_shape", [(True, [64, 512, 512, 512]),
+                                            (False, [64, 1024, 1024, 1024])])
+def test_int64_keys_4d_match_oracle_and_int32_translation(subm, big_shape):
+    """4-D clouds in grids whose key volume exceeds 2^31 (config 5 case 1's
+    [64, 512, 512, 512] for subm): 64-bit keys, tables equal to the oracle's
+    and to those of the same cloud in a small int32 grid (reference
+    tests/test_int64_linearize.py:70-120, pairs.py:166-171)."""
+    from spconv_triton.pytorch._impl import pairs as P
+
+    rng = np.random.default_rng(17)
+    small = [16, 16, 16, 16]
+    idx = rand_indices(rng, 2, [14, 14, 14, 14], 3000)
+    off = [24, 200, 300, 100]  # even: strided outputs shift by off / 2
+    big = _place(idx, off)
+    st = [1] * 4 if subm else [2] * 4
+    g_small = (small, [3] * 4, st, [1] * 4, [1] * 4, [0] * 4, subm, False)
+    g_big = (big_shape, [3] * 4, st, [1] * 4, [1] * 4, [0] * 4, subm, False)
+    out_big = big_shape if subm else [s // 2 for s in big_shape]
+    assert P.key_is_int64(2, big_shape, out_big, subm)
+    assert not P.key_is_int64(2, small, small, subm)
+    for is_train in (True, False):
+        res_b, exp_b, tb = _igemm(big, 2, g_big, is_train)
+        _compare_igemm(res_b, exp_b, tb, subm, is_train)
+    res_b, _, _ = _igemm(big, 2, g_big, True)
+    res_s, _, _ = _igemm(idx, 2, g_small, True)
+    for i in (2, 3):
+        _eq(res_b[i], res_s[i].cpu().numpy(), f"table {i} int64 vs int32")
+    for i in (4, 5, 6, 7):
+        for a, b in zip(res_b[i], res_s[i]):
+            _eq(a, b.cpu().numpy(), f"mask {i} int64 vs int32")
+    if not subm:
+        shift = np.asarray([0] + [o // 2 for o in off], np.int32)
+        _eq(res_b[0], res_s[0].cpu().numpy() + shift, "out_indices int64 vs int32")
+
+
+@pytest.mark.parametrize("gi", [0, 2, 4, 11])
+def test_unsorted_masks_bit_exact(gi):
+    """do_sort=False (reference pairs.py:386-388, SPCONV_DO_SORT=0): raw mask
+    words in row order and an identity argsort, forward and backward splits,
+    plain and MaskSplit, equal to the oracle."""
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+
+    shape, ks, st, pad, dil, op, subm, tr = GEOMS[gi]
+    rng = np.random.default_rng(5000 + gi)
+    idx = rand_indices(rng, 2, shape, max(8, int(np.prod(shape)) // 5))
+    t = torch.from_numpy(idx).to(DEV)
+    kv = int(np.prod(ks))
+    for split in ((False, True) if kv <= 32 else (False,)):
+        algo = ConvAlgo.MaskSplitImplicitGemm if split else ConvAlgo.MaskImplicitGemm
+        res = ops.get_indice_pairs_implicit_gemm(t, 2, shape, algo, ks, st, pad, dil, op, subm,
+                                                 tr, is_train=True, do_sort=False)
+        exp = orc.igemm_pairs(idx, 2, shape, ks, st, pad, dil, op, subm, tr, True,
+                              is_mask_split=split, do_sort=False)
+        _compare_igemm(res, exp, t, subm, True)
+        for ar in res[6]:
+            assert torch.equal(ar, torch.arange(ar.numel(), dtype=torch.int32, device=DEV))

@@ -16,6 +16,7 @@ import pytest
 import torch
 
 from test_gpu_gemm import CASES, _q, _tables, rand_indices
+from oracle import oracle as orc
 
 pytestmark = pytest.mark.gpu
 
@@ -161,6 +162,7 @@ def _both(a, w, bias, transpose, pairs, M, out_dtype=None):
     out_dtype = out_dtype or a.dtype
     N = w.shape[-1] if transpose else w.shape[0]
     res = []
+    prev = gemm.USE_GATHER_PLAN
     for use in (True, False):
         gemm.USE_GATHER_PLAN = use
         try:
@@ -168,7 +170,7 @@ def _both(a, w, bias, transpose, pairs, M, out_dtype=None):
             gemm._gemm(a, w, bias, transpose, pairs, M, None, None, out)
             res.append(out)
         finally:
-            gemm.USE_GATHER_PLAN = True
+            gemm.USE_GATHER_PLAN = prev
     return res
 
 
@@ -258,6 +260,7 @@ def _orders(a, w, bias, transpose, pairs, M):
 
     N = w.shape[-1] if transpose else w.shape[0]
     outs = {}
+    prev = gemm.ROW_ORDER, gemm.USE_GATHER_PLAN
     for mode in ("natural", "mask"):
         for use in (True, False):
             gemm.ROW_ORDER, gemm.USE_GATHER_PLAN = mode, use
@@ -266,7 +269,7 @@ def _orders(a, w, bias, transpose, pairs, M):
                 gemm._gemm(a, w, bias, transpose, pairs, M, None, None, out)
                 outs[(mode, use)] = out
             finally:
-                gemm.ROW_ORDER, gemm.USE_GATHER_PLAN = "auto", True
+                gemm.ROW_ORDER, gemm.USE_GATHER_PLAN = prev
     return outs
 
 
@@ -425,6 +428,26 @@ def test_mask_row_order_full_size(case):
         finally:
             gemm.ROW_ORDER = "auto"
     assert torch.equal(outs["natural"], outs["mask"])
+    order = gemm.mask_order(pf)
+    assert torch.equal(torch.sort(order.long())[0], torch.arange(n, device=DEV)), \
+        "the mask order must be a permutation of the rows"
+    if case == "subm4d":
+        # config 5 case 1 against the oracle at its stated size: the 4-D int64
+        # rulebook bit for bit, and every 40th output row of the GEMM
+        from spconv_triton.pytorch._impl import pairs as P
+
+        assert P.key_is_int64(1, shape, shape, True)
+        exp = orc.igemm_pairs(idx, 1, shape, ks, [1] * nd, [1] * nd, [1] * nd, [0] * nd, True,
+                              False, False)
+        np.testing.assert_array_equal(pf.cpu().numpy(), exp[2])
+        np.testing.assert_array_equal(res[4][0].cpu().numpy(), exp[4][0])
+        np.testing.assert_array_equal(res[6][0].cpu().numpy(), exp[6][0])
+        rows = torch.arange(0, n, 40, device=DEV)
+        ref = orc.gemm_fwd(x.double().cpu().numpy(), w.double().cpu().numpy(),
+                           pf[:, rows].cpu().numpy())
+        out = outs["natural"][rows].double().cpu().numpy()
+        bad = np.abs(out - ref) > 1e-3 * np.abs(ref) + 1e-5
+        assert not bad.any(), f"{int(bad.sum())} of {bad.size} beyond the fp16 bound"
     pf2 = pf.clone()  # a fresh table: the automatic rule decides at its second wide call
     assert gemm.row_order_variant(pf2, n, C * C) is None
     assert gemm.row_order_variant(pf2, n, C * C) is not None
@@ -448,3 +471,47 @@ def test_mask_row_order_partial_tiles(M):
     ref = outs[("natural", True)]
     for key, o in outs.items():
         assert torch.equal(o, ref), f"{key} differs from the natural planned GEMM"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_graph_replay_reads_updated_weights(dtype):
+    """A forward + input gradient captured into a HIP graph after eager warm-up
+    (packed weights cached) must read the weight's current values on every
+    replay: after w.copy_(new) the replays equal an eager call with the new
+    weight (the pack kernel is part of the graph)."""
+    from spconv_triton.pytorch._impl import gemm
+
+    rng = np.random.default_rng(12)
+    n, grid, C, K = 6000, 40, 32, 48
+    idx = rand_indices(rng, 1, [grid] * 3, n)
+    res = _tables(idx, 1, [grid] * 3, [3] * 3, [1] * 3, [1] * 3, True)
+    pf, pb = res[2], res[3]
+    torch.manual_seed(5)
+    x = torch.randn(n, C, device=DEV).to(dtype)
+    gout = torch.randn(n, K, device=DEV).to(dtype)
+    w = torch.nn.Parameter((torch.randn(K, 3, 3, 3, C, device=DEV) / np.sqrt(27 * C)).to(dtype))
+    b = torch.nn.Parameter(torch.randn(K, device=DEV).to(dtype))
+    for _ in range(2):  # warm-up: fills the packed-weight cache
+        gemm.conv_forward(x, w, pf, n, bias=b)
+        gemm.conv_backward_input(gout, w, pb, n)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            y = gemm.conv_forward(x, w, pf, n, bias=b)
+            dx = gemm.conv_backward_input(gout, w, pb, n)
+    torch.cuda.current_stream().wait_stream(s)
+    for step in range(3):
+        with torch.no_grad():
+            w.copy_((torch.randn(K, 3, 3, 3, C, device=DEV) / np.sqrt(27 * C)).to(dtype))
+            b.copy_(torch.randn(K, device=DEV).to(dtype))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        ey = gemm.conv_forward(x, w, pf, n, bias=b)
+        edx = gemm.conv_backward_input(gout, w, pb, n)
+        torch.cuda.synchronize()
+        assert torch.equal(y, ey), f"replay {step}: forward used stale weights"
+        assert torch.equal(dx, edx), f"replay {step}: dgrad used stale weights"

@@ -352,3 +352,54 @@ def test_oracle_sparse_add_golden(golden, case_id):
     np.testing.assert_array_equal(ind, expect["out_indices"].numpy())
     np.testing.assert_allclose(feats, expect["out_features"].numpy(), atol=expect["atol_out"],
                                rtol=0)
+
+
+@pytest.mark.parametrize("gi", [2, 3, 4, 5])
+def test_oracle_num_out_act_bound_subset(gi):
+    """num_out_act_bound B (reference pairs.py:318-323, its own check is the
+    subset property of tests/test_ext_conv.py:62-80): the bounded outputs
+    are the first B unbounded ones, pair_fwd is the unbounded table's first B
+    columns, pair_bwd the unbounded one with entries >= B set to -1, and the
+    masks are those of the bounded tables.  Subm ignores the bound."""
+    shape, ksize, stride, padding, dilation, out_padding, subm, transpose = GEOMS[gi]
+    rng = np.random.default_rng(500 + gi)
+    idx = _rand_indices(rng, 2, shape, max(4, int(np.prod(shape)) // 5))
+    args = (idx, 2, shape, ksize, stride, padding, dilation, out_padding, subm, transpose, True)
+    full = orc.igemm_pairs(*args)
+    n_full = full[0].shape[0]
+    for bound in (1, n_full // 3, n_full - 1, n_full, n_full + 5):
+        res = orc.igemm_pairs(*args, num_out_act_bound=bound)
+        b = min(bound, n_full)
+        np.testing.assert_array_equal(res[0], full[0][:b])
+        np.testing.assert_array_equal(res[2], full[2][:, :b])
+        np.testing.assert_array_equal(res[3], np.where(full[3] < b, full[3], -1))
+        bits = ((res[2] >= 0).astype(np.int64) << np.arange(res[2].shape[0])[:, None]).sum(0)
+        order = np.argsort(bits, kind="stable")
+        np.testing.assert_array_equal(res[6][0], order)
+        bwd_bits = ((res[3] >= 0).astype(np.int64) << np.arange(res[3].shape[0])[:, None]).sum(0)
+        np.testing.assert_array_equal(res[7][0], np.argsort(bwd_bits, kind="stable"))
+    sub = GEOMS[0]
+    s_args = (idx[:50], 2, sub[0], *sub[1:6], True, False, True)
+    np.testing.assert_array_equal(orc.igemm_pairs(*s_args, num_out_act_bound=3)[2],
+                                  orc.igemm_pairs(*s_args)[2])
+
+
+@pytest.mark.parametrize("kv", [27, 125])
+def test_oracle_masks_unsorted(kv):
+    """do_sort=False (reference pairs.py:386-388): the raw mask words of every
+    row in row order (word 0 ANDed with the split mask), the identity argsort."""
+    rng = np.random.default_rng(kv)
+    n = 2000
+    table = np.where(rng.random((kv, n)) < 0.3, 1, -1).astype(np.int32)
+    mic = (kv + 31) // 32
+    words = np.zeros((n, mic), np.int64)
+    for k in range(kv):
+        words[:, k // 32] |= (table[k] >= 0).astype(np.int64) << (k % 32)
+    splits = orc.split_masks(kv, kv <= 32)
+    pms, args = orc.mask_splits(table, splits, do_sort=False)
+    assert len(pms) == len(splits)
+    for m, pm, ar in zip(splits, pms, args):
+        exp = words.copy()
+        exp[:, 0] &= int(m[0])
+        np.testing.assert_array_equal(ar, np.arange(n, dtype=np.int32))
+        np.testing.assert_array_equal(pm.astype(np.int64) & 0xFFFFFFFF, exp)
