@@ -5,7 +5,8 @@
  * Every entry point takes plain device pointers, element counts, small host
  * structs and a HIP stream (passed as void*, i.e. a hipStream_t), and returns
  * an int status (SP_OK == 0).  Nothing here allocates device memory: callers
- * pass a workspace whose size they query first.  All work is enqueued on the
+ * pass a workspace whose size they query first (sp_conv_fwd_noalloc uses a
+ * library-held device array instead).  All work is enqueued on the
  * given stream; only sp_pairgen_conv_build() blocks the host, once, to read
  * the data-dependent output count (the reference synchronises at the same
  * point: torch.unique in spconv_triton/pytorch/_impl/pairs.py:206-209).
@@ -242,6 +243,24 @@ int sp_conv_fwd(const void* x, int32_t dtype, int64_t n_in, int64_t C,
                 const int32_t* pf, int64_t n_out, const void* bias,
                 const int32_t* pair_mask, const int32_t* mask_argsort,
                 void* out, int32_t out_dtype, void* ws, size_t ws_bytes, void* stream);
+
+/* sp_conv_fwd without the workspace argument: the relaid weights and fp32
+ * bias go into a library-held device array of SP_NOALLOC_SCRATCH_BYTES (one
+ * per GPU, kept until the process ends), so the call allocates nothing, and
+ * calls no allocating routine: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and result as sp_conv_fwd, bit for bit.  Weights
+ * whose relaid size exceeds the array (K * kv * C padded, times the element
+ * size, plus 4 * K bytes of bias) are rejected with SP_ERR_UNSUPPORTED.
+ * Every call on a GPU reuses that GPU's array: calls that overlap on one GPU
+ * (two streams, or host threads) race and must be serialised by the caller.
+ * No counterpart in the reference; it serves callers that cannot allocate. */
+#define SP_NOALLOC_SCRATCH_BYTES (8 * 1024 * 1024)
+int sp_conv_fwd_noalloc(const void* x, int32_t dtype, int64_t n_in, int64_t C,
+                        const void* w, int32_t w_dtype, int64_t K, int64_t kv,
+                        const int32_t* pf, int64_t n_out, const void* bias,
+                        const int32_t* pair_mask, const int32_t* mask_argsort,
+                        void* out, int32_t out_dtype, void* stream);
 
 /* Input gradient: dX[j, c] = sum_k sum_n G[pb[k, j], n] * W[n, k, c].
  * G [n_out, K]; pb [kv, n_in]; dX [n_in, C] in dtype.

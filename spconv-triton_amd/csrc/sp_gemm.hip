@@ -32,6 +32,7 @@
 // and read back as 16-byte MFMA operands.  The pair list of each offset is cut
 // into `splits` contiguous ranges whose fp32 partials are summed in a fixed
 // order by a second kernel (deterministic, no atomics).
+#include <mutex>
 #include <type_traits>
 
 #include "sp_common.h"
@@ -612,6 +613,42 @@ static int wgrad_splits(int64_t kv, int64_t C, int64_t K, int64_t n_rows) {
   return int(splits);
 }
 
+// ---- the forward without a caller workspace (sp_conv_fwd_noalloc) ---------
+// The relaid weights and fp32 bias, which sp_conv_fwd writes into its
+// workspace, go into this file-scope array instead: one copy per GPU, held
+// until the process ends.  Host code never passes the array's name to a
+// kernel (on the host it is only a stand-in for the symbol): the device
+// address comes from hipGetSymbolAddress, taken once per device with that
+// device current, and kernels receive that pointer.
+static_assert(SP_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch size is a multiple of 256");
+static __device__ __align__(256) unsigned char scratch[SP_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+
+// Device address of this device's `scratch` (nullptr and an error on failure).
+static void* scratch_address(int* rc) {
+  static std::mutex mu;
+  static void* addr[kMaxDevices] = {};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    *rc = set_error(SP_ERR_HIP, "fwd_noalloc: no current device (%d)", dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      *rc = set_error(SP_ERR_HIP, "fwd_noalloc: hipGetSymbolAddress(scratch) failed on device "
+                      "%d: %s", dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    addr[dev] = p;
+  }
+  *rc = SP_OK;
+  return addr[dev];
+}
+
 }  // namespace sp
 
 using namespace sp;
@@ -668,6 +705,30 @@ int sp_conv_fwd(const void* x, int32_t dtype, int64_t n_in, int64_t C, const voi
                 int32_t out_dtype, void* ws, size_t ws_bytes, void* stream) {
   return gemm_common(x, dtype, n_in, w, w_dtype, K, kv, C, 0, pf, n_out, bias, pair_mask,
                      mask_argsort, out, out_dtype, ws, ws_bytes, as_stream(stream));
+}
+
+int sp_conv_fwd_noalloc(const void* x, int32_t dtype, int64_t n_in, int64_t C, const void* w,
+                        int32_t w_dtype, int64_t K, int64_t kv, const int32_t* pf, int64_t n_out,
+                        const void* bias, const int32_t* pair_mask, const int32_t* mask_argsort,
+                        void* out, int32_t out_dtype, void* stream) {
+  SP_CHECK_ARG(gemm_dtype_ok(dtype), "fwd_noalloc: feature dtype %d not supported (f16/bf16/f32)",
+               dtype);
+  SP_CHECK_ARG(K >= 1 && C >= 1 && kv >= 1 && K < 65536 && C < 65536 && kv < 65536,
+               "fwd_noalloc: bad sizes K=%lld C=%lld kv=%lld", (long long)K, (long long)C,
+               (long long)kv);
+  const size_t need = packed_layout(K, kv, C, dtype, 0).total;
+  if (need > SP_NOALLOC_SCRATCH_BYTES)
+    return set_error(SP_ERR_UNSUPPORTED,
+                     "fwd_noalloc: relaid weights of K=%lld kv=%lld C=%lld need %zu bytes, more "
+                     "than the %d-byte scratch (use sp_conv_fwd with a workspace)",
+                     (long long)K, (long long)kv, (long long)C, need, SP_NOALLOC_SCRATCH_BYTES);
+  if (n_out == 0) return SP_OK;
+  int rc = SP_OK;
+  void* ws = scratch_address(&rc);
+  if (!ws) return rc;
+  return gemm_common(x, dtype, n_in, w, w_dtype, K, kv, C, 0, pf, n_out, bias, pair_mask,
+                     mask_argsort, out, out_dtype, ws, SP_NOALLOC_SCRATCH_BYTES,
+                     as_stream(stream));
 }
 
 int sp_conv_dgrad(const void* g, int32_t dtype, int64_t n_out, int64_t K, const void* w,

@@ -114,6 +114,8 @@ _SIGNATURES = {
     "sp_table_stats": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P]),
     "sp_conv_fwd": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _P, _I64, _P,
                                    _P, _P, _P, _I32, _P, _SZ, _P]),
+    "sp_conv_fwd_noalloc": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _P, _I64,
+                                           _P, _P, _P, _P, _I32, _P]),
     "sp_conv_dgrad": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _P, _I64, _P,
                                      _P, _P, _P, _SZ, _P]),
     "sp_wgrad_workspace_size": (_SZ, [_I64, _I64, _I64, _I64]),
