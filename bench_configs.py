@@ -13,7 +13,15 @@ weights, and prints one JSON object per configuration:
 * ``subm4d``: SubMConv4d 3^4, 128 -> 128 fp16, ~500k voxels in
   [64, 512, 512, 512], rulebook cached;
 * ``wide``: SubMConv3d 256 -> 256 fp16, 400k voxels of a 1024^3 surface
-  cloud, rulebook cached.
+  cloud, rulebook cached;
+* ``config1``: SubMConv3d 16 -> 16 fp32, 2,000 uniform voxels in 64^3,
+  rulebook rebuilt every pass (the reference's CPU-runnable case);
+* ``quickstart``: the reference README chain SubMConv3d(3 -> 32) ->
+  SparseConv3d(32 -> 64, s2) -> SparseInverseConv3d(64 -> 32), fp16 eval, 200k
+  surface voxels in 256^3, rulebooks rebuilt every pass (config 2);
+* ``lidar_c256``: SubMConv3d 256 -> 256 on a 50k-voxel LiDAR cloud, rulebook
+  cached, in fp16, IEEE fp32 and fp32 with SPCONV_ALLOW_TF32 (split-bf16
+  products), with the pairs per row and the matrix-core utilisation.
 
 Usage: ``python bench_configs.py [--config NAME ...] [--reps R]``.
 """
@@ -211,8 +219,101 @@ def cfg_wide(reps):
             "what": "SubMConv3d 256->256 fp16 forward, 1024^3 surface cloud, rulebook cached (mean)"}
 
 
+def cfg_config1(reps):
+    import spconv_triton.pytorch as spconv
+
+    from bench_data import uniform_cloud
+
+    idx = uniform_cloud(2000, [64] * 3, seed=0)
+    it = torch.from_numpy(idx).to(DEV)
+    torch.manual_seed(0)
+    feats = torch.randn(idx.shape[0], 16, device=DEV)
+    conv = spconv.SubMConv3d(16, 16, 3, padding=1, indice_key="k").to(DEV).eval()
+
+    def step():
+        with torch.no_grad():
+            return conv(spconv.SparseConvTensor(feats, it, [64] * 3, 1))
+
+    for _ in range(5):
+        step()
+    return {"voxels": int(idx.shape[0]), "median_ms": median_ms(step, 10 * reps),
+            "what": "SubMConv3d 16->16 fp32 eval, rulebook rebuilt every pass (Python host in "
+                    "the loop)"}
+
+
+def cfg_quickstart(reps):
+    import spconv_triton.pytorch as spconv
+
+    idx = surface_cloud(200_000, 256, seed=0)
+    it = torch.from_numpy(idx).to(DEV)
+    torch.manual_seed(0)
+    feats = torch.randn(idx.shape[0], 3, device=DEV).half()
+    net = spconv.SparseSequential(
+        spconv.SubMConv3d(3, 32, 3, padding=1, indice_key="subm0"),
+        spconv.SparseConv3d(32, 64, 3, stride=2, padding=1, indice_key="down0"),
+        spconv.SparseInverseConv3d(64, 32, 3, indice_key="down0"),
+    ).to(DEV).half().eval()
+
+    def step():
+        with torch.no_grad():
+            return net(spconv.SparseConvTensor(feats, it, [256] * 3, 1))
+
+    for _ in range(3):
+        step()
+    return {"voxels": int(idx.shape[0]), "median_ms": median_ms(step, reps),
+            "what": "quickstart chain fp16 eval, rulebooks rebuilt every pass"}
+
+
+def cfg_lidar_c256(reps):
+    import spconv_triton.pytorch as spconv
+    from spconv_triton import constants
+
+    shape = [41, 1600, 1408]
+    idx = lidar_cloud(50000, batch=1, seed=0, shape=shape)
+    it = torch.from_numpy(idx).to(DEV)
+    n = int(idx.shape[0])
+    out = {"voxels": n}
+    for name, dtype, tf32, peak in (("fp16", torch.float16, False, 2500.0),
+                                    ("fp32", torch.float32, False, 157.3),
+                                    ("tf32", torch.float32, True, 2500.0 / 3)):
+        torch.manual_seed(0)
+        conv = spconv.SubMConv3d(256, 256, 3, padding=1, bias=False, indice_key="k").to(DEV)
+        conv = conv.to(dtype).eval()
+        feats = torch.randn(n, 256, device=DEV).to(dtype)
+        prev = constants.SPCONV_ALLOW_TF32
+        constants.SPCONV_ALLOW_TF32 = tf32
+        try:
+            with torch.no_grad():
+                y = conv(spconv.SparseConvTensor(feats, it, shape, 1))
+                pairs = int((y.indice_dict["k"].pair_fwd >= 0).sum().item())
+                xc = spconv.SparseConvTensor(feats, it, shape, 1, indice_dict=y.indice_dict)
+                for _ in range(5):
+                    conv(xc)
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                k = 10 * reps
+                e0.record()
+                for _ in range(k):
+                    conv(xc)
+                e1.record()
+                torch.cuda.synchronize()
+                ms = e0.elapsed_time(e1) / k
+        finally:
+            constants.SPCONV_ALLOW_TF32 = prev
+        tflops = 2.0 * pairs * 256 * 256 / (ms * 1e-3) / 1e12
+        out[name] = {"ms": round(ms, 4), "pairs_per_row": round(pairs / n, 3),
+                     "useful_tflops": round(tflops, 1),
+                     "matrix_core_frac": round(tflops / peak, 4),
+                     "peak_used": {"fp16": "fp16 2.5 PFLOP/s",
+                                   "fp32": "fp32 matrix 157.3 TFLOP/s",
+                                   "tf32": "bf16 2.5 PFLOP/s / 3 products"}[name]}
+    out["what"] = "SubMConv3d 256->256 forward, rulebook cached (mean of events)"
+    return out
+
+
 CONFIGS = {"encoder": cfg_encoder, "resunet": cfg_resunet, "subm4d": cfg_subm4d,
-           "wide": cfg_wide}
+           "wide": cfg_wide, "config1": cfg_config1, "quickstart": cfg_quickstart,
+           "lidar_c256": cfg_lidar_c256}
 
 
 def main() -> int:

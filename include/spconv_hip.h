@@ -45,6 +45,12 @@ extern "C" {
 #define SP_BF16 1
 #define SP_F32 2
 #define SP_F64 3
+/* fp32 operands as bf16 parts (split-bf16, for SPCONV_ALLOW_TF32): a packed
+ * weight of this type is the SP_BF16 packing of [hi | lo | hi] along the
+ * reduction axis (3*C forward, 3*K input gradient), hi = bf16(w),
+ * lo = bf16(w - hi); the GEMM then runs as SP_BF16 over a reduction three
+ * times as long, with features split by sp_split_bf16x3 (pattern 0). */
+#define SP_BF16X3 4
 
 /* ---- pair-generation modes (spconv_triton/pytorch/_impl/pairs.py:6-22) -- */
 #define SP_PAIR_SUBM 0       /* o = x + (k//2)*d - kpos*d, o must be an input */
@@ -271,10 +277,26 @@ int sp_conv_dgrad(const void* g, int32_t dtype, int64_t n_out, int64_t K,
                   const int32_t* pair_mask, const int32_t* mask_argsort,
                   void* dx, void* ws, size_t ws_bytes, void* stream);
 
+/* Split of fp32 rows into bf16 parts for the split-bf16 products that serve
+ * SPCONV_ALLOW_TF32 (the reference runs tl.dot with input_precision="tf32" on
+ * fp32 GEMMs: gemm.py:46-71, :456-463, used by conv_forward :564,
+ * conv_backward_input :627 and conv_backward_weight :708).  x [rows, cols] f32
+ * -> out [rows, parts * cols] bf16 with hi = bf16(x), lo = bf16(x - hi):
+ * pattern 0 = [hi | hi | lo] (forward / input-gradient operand against a
+ * SP_BF16X3 packed weight: hi*hi + hi*lo + lo*hi), 1 = [hi | lo | hi],
+ * 2 = [hi | lo] (weight-gradient operands, SP_BF16X3 of sp_conv_wgrad).
+ * Each product is recovered to about 2^-16 relative (TF32: 2^-11); method of
+ * Henry, Tang & Heinecke, ARITH 2019. */
+int sp_split_bf16x3(const float* x, int64_t rows, int64_t cols, int32_t pattern, void* out,
+                    void* stream);
+
 /* Weight gradient over compacted pairs (sp_compact_table of pair_fwd):
  * dW[n, k, c] = sum_{p < counts[k]} X[in_rows[k, p], c] * G[out_rows[k, p], n].
  * X [n_in, C], G [n_out, K]; in_rows/out_rows [kv, row_stride].  Split-P fp32 partials reduced in a fixed
- * order (deterministic).  dW [K, kv, C] in dtype.
+ * order (deterministic).  dW [K, kv, C] in dtype.  dtype SP_BF16X3: x [n_in, 2C]
+ * and g [n_out, 2K] are the bf16 [hi | lo] halves of fp32 tensors (sp_split_bf16x3
+ * pattern 2), dW is fp32 (the four half products summed), and the workspace is
+ * sp_wgrad_workspace_size(2K, kv, 2C, n_rows).
  * Replaces conv_backward_weight + _dweight_masked_kernel, gemm.py:324-453, :634-713. */
 size_t sp_wgrad_workspace_size(int64_t K, int64_t kv, int64_t C, int64_t n_rows);
 int sp_conv_wgrad(const void* x, int64_t n_in, const void* g, int64_t n_out, int32_t dtype,

@@ -103,6 +103,18 @@ __device__ __forceinline__ float load_any(const void* p, int dtype, int64_t i) {
   }
 }
 
+// bf16 parts of an fp32 value v: hi = bf16(v) and lo = bf16(v - hi) (v - hi
+// is exact in fp32).  hi*hi' + hi*lo' + lo*hi' on the bf16 matrix cores, with
+// fp32 accumulation, recovers the fp32 product to about 2^-16 relative: the
+// split-bf16 method of Henry, Tang & Heinecke, "Leveraging the bfloat16
+// artificial intelligence datatype for higher-precision computations", ARITH
+// 2019.  It serves SPCONV_ALLOW_TF32 (the reference's tl.dot in TF32,
+// gemm.py:46-71, :456-463), at a precision above TF32's (2^-11).
+__device__ __forceinline__ float split_part(float v, bool lo) {
+  const float hi = float(__bf16(v));
+  return lo ? v - hi : hi;
+}
+
 // ---------------------------------------------------------------------------
 // weight relayout: KRSC [K][kv][C] -> Bt[k][r/V][n][V] (zero padded in r)
 //   forward: n = output channel (K), r = input channel (C)
@@ -110,7 +122,7 @@ __device__ __forceinline__ float load_any(const void* p, int dtype, int64_t i) {
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ void relayout_weight(const void* __restrict__ w, int w_dtype, int64_t K, int64_t kv,
-                                int64_t C, int transpose, int N, int R, int Rp,
+                                int64_t C, int transpose, int N, int R, int Rp, int split_r,
                                 T* __restrict__ bt) {
   constexpr int V = Mfma<T>::V;
   const int64_t total = kv * int64_t(Rp) * N;
@@ -122,11 +134,16 @@ __global__ void relayout_weight(const void* __restrict__ w, int w_dtype, int64_t
   t /= N;
   const int rv = int(t % (Rp / V));
   const int64_t k = t / (Rp / V);
-  const int r = rv * V + e;
+  int r = rv * V + e;
   float v = 0.f;
   if (r < R) {
+    // split_r > 0: the reduction axis holds [hi | lo | hi] of the weight's
+    // own split_r-long axis (bf16 parts of an fp32 weight, see split_part)
+    const int part = split_r ? r / split_r : 0;
+    if (split_r) r -= part * split_r;
     const int64_t src = transpose ? (int64_t(r) * kv + k) * C + n : (int64_t(n) * kv + k) * C + r;
     v = load_any(w, w_dtype, src);
+    if (split_r) v = split_part(v, part == 1);
   }
   bt[i] = from_f32<T>(v);
 }
@@ -344,12 +361,65 @@ __global__ void wgrad_reduce(const float* __restrict__ part, int splits, int64_t
   dw[i] = from_f32<T>(s);
 }
 
+// The weight gradient of split-bf16 operands (SP_BF16X3): the partials hold
+// [2K][kv][2C] = the four products of X's and G's [hi | lo] halves, which are
+// summed in a fixed order into the fp32 dW [K][kv][C].
+__global__ void wgrad_reduce_split(const float* __restrict__ part, int splits, int64_t K,
+                                   int64_t kv, int64_t C, float* __restrict__ dw) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = K * kv * C;
+  if (i >= total) return;
+  const int64_t c = i % C, nk = i / C, k = nk % kv, n = nk / kv;
+  const int64_t part_total = 4 * total;
+  float s = 0.f;
+  for (int p = 0; p < splits; ++p)
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+        s += part[int64_t(p) * part_total + ((a * K + n) * kv + k) * 2 * C + b * C + c];
+  dw[i] = s;
+}
+
+// out [rows][parts * cols] bf16 from x [rows][cols] fp32: pattern 0 = [hi |
+// hi | lo], 1 = [hi | lo | hi], 2 = [hi | lo] (split_part).  Four columns per
+// thread with vec4 (cols % 4 == 0, x 16-byte and out 8-byte aligned).
+__global__ void split_bf16_rows(const float* __restrict__ x, int64_t rows, int64_t cols,
+                                int pattern, bool vec4, __bf16* __restrict__ out) {
+  const int parts = pattern == 2 ? 2 : 3;
+  const int64_t per_row = vec4 ? cols / 4 : cols;
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= rows * per_row) return;
+  const int64_t row = i / per_row, q = i % per_row;
+  const int width = vec4 ? 4 : 1;
+  const int64_t c0 = q * width;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  if (vec4) {
+    const float4 f = *reinterpret_cast<const float4*>(x + row * cols + c0);
+    v[0] = f.x; v[1] = f.y; v[2] = f.z; v[3] = f.w;
+  } else {
+    v[0] = x[row * cols + c0];
+  }
+  __bf16* o = out + row * parts * cols + c0;
+  for (int pi = 0; pi < parts; ++pi) {
+    const bool lo = pattern == 0 ? pi == 2 : pi == 1;
+    __bf16 h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = __bf16(split_part(v[e], lo));
+    if (vec4) {
+      *reinterpret_cast<uint2*>(o + pi * cols) = __builtin_bit_cast(uint2, h);
+    } else {
+      o[pi * cols] = h[0];
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 static int elem_size(int dtype) {
   switch (dtype) {
-    case SP_F16: case SP_BF16: return 2;
+    case SP_F16: case SP_BF16: case SP_BF16X3: return 2;
     case SP_F32: return 4;
     case SP_F64: return 8;
     default: return 0;
@@ -367,10 +437,12 @@ struct Packed {
   size_t bt_bytes, bias_off, total;
 };
 
+// SP_BF16X3 (the split-bf16 form of an fp32 weight) is the SP_BF16 layout of a
+// reduction three times as long: [hi | lo | hi] along C (forward) or K (dgrad).
 static Packed packed_layout(int64_t K, int64_t kv, int64_t C, int dtype, int transpose) {
   Packed p;
   p.N = int(transpose ? C : K);
-  p.R = int(transpose ? K : C);
+  p.R = int(transpose ? K : C) * (dtype == SP_BF16X3 ? 3 : 1);
   // the reduction runs in MFMA steps of 4 * V (four lane groups of V each)
   p.Rp = int(padded(p.R, 4 * vec_of(dtype)));
   p.bt_bytes = size_t(kv) * size_t(p.Rp) * size_t(p.N) * size_t(elem_size(dtype));
@@ -383,7 +455,8 @@ static bool gemm_dtype_ok(int dtype) { return dtype == SP_F16 || dtype == SP_BF1
 
 static int pack_weight(const void* w, int w_dtype, const void* bias, int64_t K, int64_t kv,
                        int64_t C, int dtype, int transpose, void* packed, hipStream_t s) {
-  SP_CHECK_ARG(gemm_dtype_ok(dtype), "pack: compute dtype %d not supported (f16/bf16/f32)", dtype);
+  SP_CHECK_ARG(gemm_dtype_ok(dtype) || dtype == SP_BF16X3,
+               "pack: compute dtype %d not supported (f16/bf16/f32/bf16x3)", dtype);
   SP_CHECK_ARG(elem_size(w_dtype) > 0, "pack: weight dtype %d not supported", w_dtype);
   SP_CHECK_ARG(K >= 1 && C >= 1 && kv >= 1 && K < 65536 && C < 65536 && kv < 65536,
                "pack: bad sizes K=%lld kv=%lld C=%lld", (long long)K, (long long)kv, (long long)C);
@@ -395,15 +468,19 @@ static int pack_weight(const void* w, int w_dtype, const void* bias, int64_t K, 
   switch (dtype) {
     case SP_F16:
       relayout_weight<_Float16><<<rb, 256, 0, s>>>(w, w_dtype, K, kv, C, transpose, p.N, p.R,
-                                                   p.Rp, reinterpret_cast<_Float16*>(base));
+                                                   p.Rp, 0, reinterpret_cast<_Float16*>(base));
       break;
     case SP_BF16:
       relayout_weight<__bf16><<<rb, 256, 0, s>>>(w, w_dtype, K, kv, C, transpose, p.N, p.R, p.Rp,
-                                                 reinterpret_cast<__bf16*>(base));
+                                                 0, reinterpret_cast<__bf16*>(base));
+      break;
+    case SP_BF16X3:
+      relayout_weight<__bf16><<<rb, 256, 0, s>>>(w, w_dtype, K, kv, C, transpose, p.N, p.R, p.Rp,
+                                                 p.R / 3, reinterpret_cast<__bf16*>(base));
       break;
     default:
       relayout_weight<float><<<rb, 256, 0, s>>>(w, w_dtype, K, kv, C, transpose, p.N, p.R, p.Rp,
-                                                reinterpret_cast<float*>(base));
+                                                0, reinterpret_cast<float*>(base));
   }
   SP_LAUNCHED();
   bias_to_f32<<<unsigned(cdiv(p.N, 256)), 256, 0, s>>>(bias, w_dtype, p.N,
@@ -748,29 +825,33 @@ int sp_conv_wgrad(const void* x, int64_t n_in, const void* g, int64_t n_out, int
                   int64_t C, int64_t K, int64_t kv, const int32_t* in_rows,
                   const int32_t* out_rows, const int32_t* counts, int64_t row_stride, void* dw,
                   void* ws, size_t ws_bytes, void* stream) {
-  SP_CHECK_ARG(dtype == SP_F16 || dtype == SP_BF16 || dtype == SP_F32,
-               "wgrad: dtype %d not supported (f16/bf16/f32)", dtype);
+  SP_CHECK_ARG(dtype == SP_F16 || dtype == SP_BF16 || dtype == SP_F32 || dtype == SP_BF16X3,
+               "wgrad: dtype %d not supported (f16/bf16/f32/bf16x3)", dtype);
   SP_CHECK_ARG(K >= 1 && C >= 1 && kv >= 1 && row_stride >= 0, "wgrad: bad sizes");
-  SP_CHECK_ARG(K < 65536 && C < 65536 && kv < 65536, "wgrad: channel/kernel size too large");
   SP_CHECK_ARG(x && g && in_rows && out_rows && counts && dw, "wgrad: null pointer");
   hipStream_t s = as_stream(stream);
-  const int splits = wgrad_splits(kv, C, K, row_stride);
-  const size_t need = sp_wgrad_workspace_size(K, kv, C, row_stride);
+  // split-bf16 operands: X [n_in, 2C] and G [n_out, 2K] bf16 halves [hi | lo]
+  const bool split = dtype == SP_BF16X3;
+  const int64_t Cg = split ? 2 * C : C, Kg = split ? 2 * K : K;
+  SP_CHECK_ARG(Kg < 65536 && Cg < 65536 && kv < 65536, "wgrad: channel/kernel size too large");
+  const int elem = split ? SP_BF16 : dtype;
+  const int splits = wgrad_splits(kv, Cg, Kg, row_stride);
+  const size_t need = sp_wgrad_workspace_size(Kg, kv, Cg, row_stride);
   if (!ws || ws_bytes < need)
     return set_error(SP_ERR_WORKSPACE, "wgrad: workspace %zu < %zu", ws_bytes, need);
   float* part = static_cast<float*>(ws);
   const int64_t gx = kv * splits;
   SP_CHECK_ARG(gx <= kMaxGridX, "wgrad: grid too large");
-  const int64_t es = dtype == SP_F32 ? 4 : 2;
-  const int64_t xb = n_in * C * es, gb = n_out * K * es;
+  const int64_t es = elem == SP_F32 ? 4 : 2;
+  const int64_t xb = n_in * Cg * es, gb = n_out * Kg * es;
   if (xb >= int64_t(kOob) || gb >= int64_t(kOob))
     return set_error(SP_ERR_UNSUPPORTED, "wgrad: features exceed 4 GiB");
   // 16-byte row gathers need whole vectors per row and aligned bases
-  const int v = vec_of(dtype);
-  const int vec = (C % v == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 ? 1 : 0) |
-                  (K % v == 0 && reinterpret_cast<uintptr_t>(g) % 16 == 0 ? 2 : 0);
-  const int bw = wgrad_block(C, K);
-  dim3 grid(unsigned(gx), unsigned(cdiv(C, bw)), unsigned(cdiv(K, bw)));
+  const int v = vec_of(elem);
+  const int vec = (Cg % v == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 ? 1 : 0) |
+                  (Kg % v == 0 && reinterpret_cast<uintptr_t>(g) % 16 == 0 ? 2 : 0);
+  const int bw = wgrad_block(Cg, Kg);
+  dim3 grid(unsigned(gx), unsigned(cdiv(Cg, bw)), unsigned(cdiv(Kg, bw)));
   const int64_t tot = K * kv * C;
   const unsigned rb = unsigned(cdiv(tot, 256));
   auto run = [&](auto tag) {
@@ -782,15 +863,35 @@ int sp_conv_wgrad(const void* x, int64_t n_in, const void* g, int64_t n_out, int
                           wgrad_partial<T, 2, 128>, wgrad_partial<T, 3, 128>};
     const Kern kern = bw == 128 ? k128[vec] : k64[vec];
     kern<<<grid, 256, 0, s>>>(static_cast<const T*>(x), n_in, static_cast<const T*>(g), n_out,
-                              int(C), int(K), int(kv), in_rows, out_rows, counts, row_stride,
+                              int(Cg), int(Kg), int(kv), in_rows, out_rows, counts, row_stride,
                               splits, part, uint32_t(xb), uint32_t(gb));
-    wgrad_reduce<T><<<rb, 256, 0, s>>>(part, splits, tot, static_cast<T*>(dw));
+    if (split)
+      wgrad_reduce_split<<<rb, 256, 0, s>>>(part, splits, K, kv, C, static_cast<float*>(dw));
+    else
+      wgrad_reduce<T><<<rb, 256, 0, s>>>(part, splits, tot, static_cast<T*>(dw));
   };
-  switch (dtype) {
+  switch (elem) {
     case SP_F16: run(_Float16{}); break;
     case SP_BF16: run(__bf16{}); break;
     default: run(float{});
   }
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+int sp_split_bf16x3(const float* x, int64_t rows, int64_t cols, int32_t pattern, void* out,
+                    void* stream) {
+  SP_CHECK_ARG(rows >= 0 && cols >= 1 && pattern >= 0 && pattern <= 2,
+               "split_bf16x3: bad sizes or pattern (rows=%lld cols=%lld pattern=%d)",
+               (long long)rows, (long long)cols, pattern);
+  if (rows == 0) return SP_OK;
+  SP_CHECK_ARG(x && out, "split_bf16x3: null pointer");
+  const bool vec4 = cols % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(out) % 8 == 0;
+  const int64_t work = rows * (vec4 ? cols / 4 : cols);
+  SP_CHECK_ARG(cdiv(work, 256) <= kMaxGridX, "split_bf16x3: too many elements");
+  split_bf16_rows<<<unsigned(cdiv(work, 256)), 256, 0, as_stream(stream)>>>(
+      x, rows, cols, pattern, vec4, static_cast<__bf16*>(out));
   SP_LAUNCHED();
   return SP_OK;
 }

@@ -32,6 +32,8 @@ SP_ERR_HASH_FULL = 5
 SP_F16, SP_BF16, SP_F32, SP_F64 = 0, 1, 2, 3
 SP_PAIR_SUBM, SP_PAIR_REGULAR, SP_PAIR_TRANSPOSE = 0, 1, 2
 
+SP_BF16X3 = 4  # fp32 operands as split-bf16 parts (SPCONV_ALLOW_TF32)
+
 _DTYPE_CODE = {
     torch.float16: SP_F16,
     torch.bfloat16: SP_BF16,
@@ -118,6 +120,7 @@ _SIGNATURES = {
                                            _P, _P, _P, _P, _I32, _P]),
     "sp_conv_dgrad": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _P, _I64, _P,
                                      _P, _P, _P, _SZ, _P]),
+    "sp_split_bf16x3": (ctypes.c_int, [_P, _I64, _I64, _I32, _P, _P]),
     "sp_wgrad_workspace_size": (_SZ, [_I64, _I64, _I64, _I64]),
     "sp_conv_wgrad": (ctypes.c_int, [_P, _I64, _P, _I64, _I32, _I64, _I64, _I64, _P, _P, _P,
                                      _I64, _P, _P, _SZ, _P]),

@@ -5,12 +5,18 @@ Host-side mirror of ``spconv_triton/pytorch/_impl/gemm.py`` of the reference
 ``conv_backward_weight`` :634-713).  The device work is the MFMA gather-GEMM of
 ``csrc/sp_gemm.hip``.
 
-Precision: every GEMM accumulates in fp32 on the matrix cores.  The
-reference's optional fp16 accumulation (``SPCONV_ALLOW_FP16_ACCUM`` /
-``fp32_accum=False``) and TF32 (``SPCONV_ALLOW_TF32``) are speed knobs that
-relax precision; on gfx950 there is no fp16-accumulating or xf32 MFMA, so
-both requests are served at full fp32 accumulation / IEEE fp32, which is at
-least as accurate.  The flags are still accepted.
+Precision: every GEMM accumulates in fp32 on the matrix cores.
+
+* ``SPCONV_ALLOW_TF32`` (read live, fp32 tensors only, like the reference's
+  ``_allow_tf32``, gemm.py:456-463): the forward, input-gradient and
+  weight-gradient GEMMs run as split-bf16 products on the bf16 matrix cores
+  (gfx950 has no xf32 MFMA).  Each fp32 operand x becomes hi = bf16(x) and
+  lo = bf16(x - hi), and hi*hi + hi*lo + lo*hi recovers each product to about
+  2^-16 relative, tighter than TF32's 2^-11 (Henry, Tang & Heinecke, ARITH
+  2019).  Off (the default), fp32 GEMMs are IEEE fp32.
+* ``SPCONV_ALLOW_FP16_ACCUM`` / ``fp32_accum=False`` ask for fp16
+  accumulation; gfx950 has no fp16-accumulating MFMA, so they are served at
+  fp32 accumulation, which is at least as accurate.  The flags are accepted.
 """
 
 from __future__ import annotations
@@ -22,6 +28,26 @@ import weakref
 import torch
 
 from . import _lib
+
+
+def _tf32(t: torch.Tensor) -> bool:
+    """Split-bf16 products for an fp32 GEMM: live ``SPCONV_ALLOW_TF32`` (reference
+    ``_allow_tf32``, gemm.py:460-463)."""
+    from spconv_triton import constants
+
+    return t.dtype == torch.float32 and bool(constants.SPCONV_ALLOW_TF32)
+
+
+def split_bf16(x: torch.Tensor, pattern: int) -> torch.Tensor:
+    """bf16 parts of fp32 rows (``sp_split_bf16x3``): pattern 0 = [hi | hi | lo],
+    1 = [hi | lo | hi], 2 = [hi | lo]; returns [rows, parts * cols] bf16."""
+    x = x.contiguous()
+    rows, cols = x.shape
+    parts = 2 if pattern == 2 else 3
+    out = torch.empty((rows, parts * cols), dtype=torch.bfloat16, device=x.device)
+    _lib.check(_lib.lib().sp_split_bf16x3(_lib.ptr(x), rows, cols, pattern, _lib.ptr(out),
+                                          _lib.stream_of(x.device)), "sp_split_bf16x3")
+    return out
 
 
 def _should_mask(kv: int, pmask, argsort) -> bool:
@@ -66,9 +92,10 @@ class _PackCache:
 _PACKED = _PackCache()
 
 
-def packed_weight(filters: torch.Tensor, bias: torch.Tensor | None, dtype: torch.dtype,
+def packed_weight(filters: torch.Tensor, bias: torch.Tensor | None, dtype,
                   transpose: bool) -> torch.Tensor:
-    """Weights (+ bias) relaid into the MFMA operand layout of ``dtype``; see
+    """Weights (+ bias) relaid into the MFMA operand layout of ``dtype`` (a torch
+    dtype, or "bf16x3": the split-bf16 form of an fp32 weight); see
     ``sp_conv_pack_weight``.  filters is KRSC [K, *ksize, C].
 
     While the stream is being captured into a graph the cache is bypassed: the
@@ -87,7 +114,7 @@ def packed_weight(filters: torch.Tensor, bias: torch.Tensor | None, dtype: torch
     if b is not None and b.dtype != w.dtype:
         b = b.to(w.dtype)
     L = _lib.lib()
-    dt = _lib.dtype_code(dtype)
+    dt = _lib.SP_BF16X3 if dtype == "bf16x3" else _lib.dtype_code(dtype)
     packed = torch.empty(L.sp_conv_packed_bytes(K, kv, C, dt, int(transpose)), dtype=torch.uint8,
                          device=w.device)
     _lib.check(L.sp_conv_pack_weight(_lib.ptr(w), _lib.dtype_code(w.dtype), _lib.ptr(b), K, kv,
@@ -258,13 +285,18 @@ def plan_overflow_count(plan: torch.Tensor) -> int:
 
 
 def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: torch.Tensor,
-          M: int, pm, ar, out: torch.Tensor):
+          M: int, pm, ar, out: torch.Tensor, split: bool = False):
+    """out = gather-GEMM of ``a`` through ``pairs``.  split: ``a`` is the
+    [hi | hi | lo] split of an fp32 operand (``split_bf16`` pattern 0) and the
+    weight is packed as "bf16x3", so the reduction runs three times as long."""
     K, C = filters.shape[0], filters.shape[-1]
     kv = pairs.shape[0]
-    packed = packed_weight(filters, bias, a.dtype, transpose)
+    packed = packed_weight(filters, bias, "bf16x3" if split else a.dtype, transpose)
     L = _lib.lib()
     use_plan = _use_plan(M, C, K)
     variant = row_order_variant(pairs, a.shape[0], K * C, use_plan)
+    if split:  # the GEMM's reduction dimension is tripled
+        K, C = (3 * K, C) if transpose else (K, 3 * C)
     if variant is not None:
         order, perm, plan = variant
         _lib.check(L.sp_conv_gemm_ordered(
@@ -318,6 +350,9 @@ def conv_forward(features: torch.Tensor, filters_krsc: torch.Tensor, pair_fwd: t
     ar = mask_argsort.contiguous() if use_mask else None
     if use_mask and (pm.numel() != n_out or ar.numel() != n_out):
         raise AssertionError("mask tables do not match the output rows")
+    if _tf32(x):
+        _gemm(split_bf16(x, 0), filters_krsc, bias, False, pf, n_out, pm, ar, out, split=True)
+        return out
     _gemm(x, filters_krsc, bias, False, pf, n_out, pm, ar, out)
     return out
 
@@ -343,6 +378,9 @@ def conv_backward_input(grad_out: torch.Tensor, filters_krsc: torch.Tensor,
     use_mask = _should_mask(kv, pair_mask, mask_argsort)
     pm = pair_mask.contiguous() if use_mask else None
     ar = mask_argsort.contiguous() if use_mask else None
+    if _tf32(g):
+        _gemm(split_bf16(g, 0), filters_krsc, None, True, pb, n_in, pm, ar, din, split=True)
+        return din
     _gemm(g, filters_krsc, None, True, pb, n_in, pm, ar, din)
     return din
 
@@ -388,9 +426,14 @@ def conv_backward_weight(features: torch.Tensor, grad_out: torch.Tensor, pair_fw
     in_rows, out_rows, counts = compacted_signal(pair_fwd)
     stride = in_rows.shape[1]
     L = _lib.lib()
-    ws = _lib.workspace(L.sp_wgrad_workspace_size(K, kv, C, stride), x.device)
+    dt = _lib.dtype_code(x.dtype)
+    if _tf32(x):  # split-bf16 halves [hi | lo]; the fp32 dW sums their four products
+        x, g, dt = split_bf16(x, 2), split_bf16(g, 2), _lib.SP_BF16X3
+        ws = _lib.workspace(L.sp_wgrad_workspace_size(2 * K, kv, 2 * C, stride), x.device)
+    else:
+        ws = _lib.workspace(L.sp_wgrad_workspace_size(K, kv, C, stride), x.device)
     _lib.check(L.sp_conv_wgrad(_lib.ptr(x), x.shape[0], _lib.ptr(g), n_out,
-                               _lib.dtype_code(x.dtype), C, K, kv, _lib.ptr(in_rows),
+                               dt, C, K, kv, _lib.ptr(in_rows),
                                _lib.ptr(out_rows), _lib.ptr(counts), stride, _lib.ptr(dw),
                                _lib.ptr(ws), ws.numel(), _lib.stream_of(x.device)),
                "sp_conv_wgrad")
