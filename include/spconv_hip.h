@@ -100,6 +100,26 @@ int sp_pairgen_subm(const sp_geom* g, const int32_t* indices, int64_t n,
                     int32_t* pair_fwd, int32_t* pair_bwd, uint32_t* mask_words,
                     void* ws, size_t ws_bytes, void* stream);
 
+/* Int32 entries of the dense cell -> row grid buffer that sp_pairgen_subm_grid
+ * needs for this geometry and n rows (the cells plus 4 guard entries on either
+ * side), or 0 when that path does not apply (volume above 2^26 cells or 256
+ * cells per row, n >= 2^24, kv > 512, not subm). */
+int64_t sp_pairgen_subm_grid_cells(const sp_geom* g, int64_t n);
+
+/* sp_pairgen_subm on a caller-kept grid, without clearing it: the grid
+ * (grid_cells >= sp_pairgen_subm_grid_cells int32 cells) holds stamps of
+ * earlier builds, each below `epoch` (1..255) in its top byte -- the caller
+ * zero-fills a new grid, then uses epochs 1, 2, ... and fills it again before
+ * reusing epoch values.  Writes the same pair_fwd / pair_bwd / mask_words as
+ * sp_pairgen_subm and, when npl is not null, zeros npl[kv] (the
+ * indice_num_per_loc of the implicit-GEMM tuple).  Calls that share a grid must
+ * not overlap (one grid per stream).  Replaces the same reference functions as
+ * sp_pairgen_subm (spconv_triton/pytorch/_impl/pairs.py:126-220, :281-426),
+ * without the per-build clear of the lookup structure. */
+int sp_pairgen_subm_grid(const sp_geom* g, const int32_t* indices, int64_t n, int32_t* pair_fwd,
+                         int32_t* pair_bwd, uint32_t* mask_words, int32_t* npl, int32_t* grid,
+                         int64_t grid_cells, uint32_t epoch, void* stream);
+
 /* Regular / transposed convolution, phase 1: deduplicate the candidate output
  * keys, sort them ascending (batch-major linear key), and rank them.  Blocks
  * until the count is known and stores it in *n_out (0 = every point vanished).

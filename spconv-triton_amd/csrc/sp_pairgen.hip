@@ -313,6 +313,187 @@ __global__ __launch_bounds__(256) void subm_probe_dense(const int32_t* __restric
   }
 }
 
+// ---- dense-grid probe with per-offset tables ---------------------------------
+// The same outputs as subm_probe_dense, in 32-bit arithmetic (a dense grid has
+// at most kDenseMaxCells < 2^31 cells): the kernel window's per-dimension
+// displacements and linear key displacements are tabulated once per workgroup
+// in LDS, so a lookup is a bounds test per dimension and one load, and all of a
+// row's lookups (up to kProbeBatch) are in flight together.
+//
+// EPOCH grids hold stamped cells, (epoch << 24) | (0xFFFFFF - row): a cell is
+// occupied in this build iff its stamp is the build's epoch (the caller keeps
+// the grid between builds and moves to a new epoch for each, so cells of
+// earlier builds read as empty with no fill), and atomicMax on the stamp keeps
+// the smallest row of a cell, as atomicMin does on a filled grid.
+constexpr int kProbeMaxKv = 512;  // a multiple of kProbeBatch
+constexpr int64_t kGridPad = 4;  // cells before a grid's first and after its last one
+constexpr int kProbeBatch = 32;
+constexpr int32_t kStampRowBits = 24;
+constexpr int32_t kStampRowMask = (1 << kStampRowBits) - 1;
+
+__device__ __forceinline__ bool grid_base(const int32_t* __restrict__ idx, int32_t r,
+                                          const GeomDev& g, int32_t (&x)[4], int32_t* base) {
+  // every load first, then the checks (short-circuit tests between the loads
+  // would wait for each one in turn); bitwise &, not &&, for the same reason
+  const int32_t* p = idx + int64_t(r) * (g.ndim + 1);
+  int32_t c[5];
+  c[0] = p[0];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) c[d + 1] = d < g.ndim ? p[d + 1] : 0;
+  bool ok = (c[0] >= 0) & (c[0] < int32_t(g.batch));
+  int32_t acc = c[0];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    x[d] = c[d + 1];
+    if (d < g.ndim) {
+      ok = ok & (uint32_t(x[d]) < uint32_t(g.in_shape[d]));
+      acc = acc * int32_t(g.in_shape[d]) + x[d];
+    }
+  }
+  *base = acc;
+  return ok;
+}
+
+template <bool EPOCH>
+__global__ __launch_bounds__(256) void subm_insert_grid(const int32_t* __restrict__ idx,
+                                                        int32_t n, GeomDev g,
+                                                        int32_t* __restrict__ grid,
+                                                        uint32_t epoch) {
+  const int32_t r = int32_t(blockIdx.x) * int32_t(blockDim.x) + int32_t(threadIdx.x);
+  if (r >= n) return;
+  int32_t x[4], key;
+  if (!grid_base(idx, r, g, x, &key)) return;
+  if (EPOCH)
+    atomicMax(reinterpret_cast<uint32_t*>(grid) + key,
+              (epoch << kStampRowBits) | uint32_t(kStampRowMask - r));
+  else
+    atomicMin(grid + key, r);
+}
+
+// RUN = 3 (last kernel dimension 3 wide, dilation 1): the three cells of a
+// run of offsets along the last dimension are adjacent in the grid and come
+// in one 12-byte load, which touches one or two cache lines where three 4-byte
+// loads touch up to three: with the rows of a wave spread over many grid lines,
+// the number of lines a load instruction touches is what the lookups cost.
+// RUN = 1: one cell per load, any window.  A grid buffer holds kGridPad cells
+// before cell 0 and after the last cell (`grid` points at cell 0), so a run's
+// load starts and ends inside the buffer: a buffer load starting out of range
+// reads zeros in all three lanes, in range or not.
+template <bool EPOCH, int RUN>
+__global__ __launch_bounds__(256) void subm_probe_grid(
+    const int32_t* __restrict__ idx, int32_t n, GeomDev g, const int32_t* __restrict__ grid,
+    uint32_t grid_bytes, uint32_t epoch, int32_t* __restrict__ pf, int32_t* __restrict__ pb,
+    uint32_t* __restrict__ words, int mic, int32_t* __restrict__ npl) {
+  static_assert(RUN == 1 || RUN == 3, "runs of 1 or 3 cells");
+  constexpr int kRunBatch = kProbeBatch / RUN;  // runs per batch of lookups
+  // per run: displacement of its first cell per dimension and linear
+  // displacement; the runs past the last one, up to a whole batch, fail every
+  // bounds test, so the lookup loop runs whole batches without a branch
+  __shared__ int32_t s_lin[kProbeMaxKv];
+  __shared__ int32_t s_disp[kProbeMaxKv][4];
+  const int kv = g.kv;
+  const int nruns = kv / RUN;
+  const int nrb = (nruns + kRunBatch - 1) / kRunBatch * kRunBatch;
+  for (int j = threadIdx.x; j < nrb; j += blockDim.x) {
+    int rem = j * RUN, lin = 0, stride = 1;
+    int disp[4] = {0, 0, 0, 0};
+    for (int d = g.ndim - 1; d >= 0; --d) {
+      const int o = rem % g.ks[d];
+      rem /= g.ks[d];
+      disp[d] = j < nruns ? o * g.dil[d] - g.pad[d] : int(g.in_shape[d]);  // padding: out of range
+      lin += disp[d] * stride;
+      stride *= int(g.in_shape[d]);
+    }
+#pragma unroll
+    for (int d = 0; d < 4; ++d) s_disp[j][d] = disp[d];
+    s_lin[j] = lin;
+  }
+  if (npl && blockIdx.x == 0)
+    for (int k = threadIdx.x; k < kv; k += blockDim.x) npl[k] = 0;
+  __syncthreads();
+  const int32_t r = int32_t(blockIdx.x) * int32_t(blockDim.x) + int32_t(threadIdx.x);
+  if (r >= n) return;
+  int32_t x[4], base;
+  const bool ok = grid_base(idx, r, g, x, &base);
+  uint32_t shape[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) shape[d] = d < g.ndim ? uint32_t(g.in_shape[d]) : 1u;
+  const int last = g.ndim - 1;
+  const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t*>(grid - kGridPad), (short)0, int(grid_bytes), 0x00020000);
+  uint32_t word = 0;
+  for (int j0 = 0; j0 < nruns; j0 += kRunBatch) {
+    int32_t v[kRunBatch][RUN];
+    bool in[kRunBatch][RUN];
+#pragma unroll
+    for (int u = 0; u < kRunBatch; ++u) {
+      const int j = j0 + u;
+      // all dimensions but the run's own (the last one, when RUN > 1)
+      bool b = ok;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        if (RUN == 1 || d != last) b = b & (uint32_t(x[d] + s_disp[j][d]) < shape[d]);
+      const uint32_t off =
+          b ? uint32_t(base + s_lin[j] + int32_t(kGridPad)) * 4u : 0xFFFFFFF0u;  // else 0s
+      if constexpr (RUN == 3) {
+        const auto t3 = __builtin_amdgcn_raw_buffer_load_b96(rg, off, 0, 0);
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+          v[u][t] = int32_t(t3[t]);
+          in[u][t] = b & (uint32_t(x[last] + s_disp[j][last] + t) < shape[last]);
+        }
+      } else {
+        v[u][0] = int32_t(__builtin_amdgcn_raw_buffer_load_b32(rg, off, 0, 0));
+        in[u][0] = b;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kRunBatch; ++u) {
+#pragma unroll
+      for (int t = 0; t < RUN; ++t) {
+        const int k = (j0 + u) * RUN + t;
+        if (k < kv) {
+          int32_t jr;
+          if (EPOCH)
+            jr = in[u][t] && (uint32_t(v[u][t]) >> kStampRowBits) == epoch
+                     ? kStampRowMask - (v[u][t] & kStampRowMask)
+                     : -1;
+          else
+            jr = in[u][t] && v[u][t] != kNoRow ? v[u][t] : -1;
+          if (pf) pf[int64_t(k) * n + r] = jr;
+          if (pb) pb[int64_t(kv - 1 - k) * n + r] = jr;
+          if (jr >= 0) word |= 1u << (k & 31);
+          if ((k & 31) == 31 || k == kv - 1) {
+            if (words) words[int64_t(r) * mic + (k >> 5)] = word;
+            word = 0;
+          }
+        }
+      }
+    }
+  }
+}
+
+// Whether the probe takes runs of 3 cells along the last dimension.
+static bool probe_runs3(const GeomDev& g) {
+  return g.ks[g.ndim - 1] == 3 && g.dil[g.ndim - 1] == 1;
+}
+
+template <bool EPOCH>
+static int launch_probe_grid(const int32_t* idx, int64_t n, const GeomDev& d,
+                             const int32_t* grid, int64_t cells, uint32_t epoch, int32_t* pf,
+                             int32_t* pb, uint32_t* words, int mic, int32_t* npl, hipStream_t s) {
+  const unsigned blocks = unsigned(cdiv(n, 256));
+  const uint32_t bytes = uint32_t((cells + 2 * kGridPad) * 4);  // the whole buffer
+  if (probe_runs3(d))
+    subm_probe_grid<EPOCH, 3><<<blocks, 256, 0, s>>>(idx, int32_t(n), d, grid, bytes, epoch, pf,
+                                                     pb, words, mic, npl);
+  else
+    subm_probe_grid<EPOCH, 1><<<blocks, 256, 0, s>>>(idx, int32_t(n), d, grid, bytes, epoch, pf,
+                                                     pb, words, mic, npl);
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
 // ---------------------------------------------------------------------------
 // regular / transpose
 // ---------------------------------------------------------------------------
@@ -722,7 +903,7 @@ size_t sp_pairgen_workspace_size(const sp_geom* g, int64_t n) {
   if (d.mode == SP_PAIR_SUBM) {
     WsSizerP z;
     if (subm_dense(d, n)) {
-      z.take<int32_t>(size_t(subm_cells(d)));
+      z.take<int32_t>(size_t(subm_cells(d) + 2 * kGridPad));
       return z.off;
     }
     void* ta;
@@ -760,10 +941,17 @@ int sp_pairgen_subm(const sp_geom* g, const int32_t* indices, int64_t n, int32_t
   const unsigned blocks = unsigned(cdiv(n, 256));
   if (subm_dense(d, n)) {
     const int64_t cells = subm_cells(d);
-    int32_t* grid = c.take<int32_t>(size_t(cells));
-    const int64_t fb = cdiv(cdiv(cells, 4), 256);
-    fill_i32x4<<<unsigned(fb < 4096 ? fb : 4096), 256, 0, s>>>(grid, cells, kNoRow);
+    int32_t* buf = c.take<int32_t>(size_t(cells + 2 * kGridPad));
+    int32_t* grid = buf + kGridPad;  // cell 0
+    const int64_t fb = cdiv(cdiv(cells + 2 * kGridPad, 4), 256);
+    fill_i32x4<<<unsigned(fb < 4096 ? fb : 4096), 256, 0, s>>>(buf, cells + 2 * kGridPad, kNoRow);
     SP_LAUNCHED();
+    if (d.kv <= kProbeMaxKv) {
+      subm_insert_grid<false><<<blocks, 256, 0, s>>>(indices, int32_t(n), d, grid, 0u);
+      SP_LAUNCHED();
+      return launch_probe_grid<false>(indices, n, d, grid, cells, 0u, pair_fwd, pair_bwd,
+                                      mask_words, mic, nullptr, s);
+    }
     subm_insert_dense<<<blocks, 256, 0, s>>>(indices, n, d, grid);
     SP_LAUNCHED();
     subm_probe_dense<<<blocks, 256, 0, s>>>(indices, n, d, grid, pair_fwd, pair_bwd, mask_words,
@@ -794,6 +982,37 @@ int sp_pairgen_subm(const sp_geom* g, const int32_t* indices, int64_t n, int32_t
     SP_LAUNCHED();
   }
   return SP_OK;
+}
+
+int64_t sp_pairgen_subm_grid_cells(const sp_geom* g, int64_t n) {
+  GeomDev d;
+  if (make_geom(g, &d) != SP_OK) return 0;
+  if (d.mode != SP_PAIR_SUBM || n < 1 || n > kStampRowMask || d.kv > kProbeMaxKv) return 0;
+  return subm_dense(d, n) ? subm_cells(d) + 2 * kGridPad : 0;
+}
+
+int sp_pairgen_subm_grid(const sp_geom* g, const int32_t* indices, int64_t n, int32_t* pair_fwd,
+                         int32_t* pair_bwd, uint32_t* mask_words, int32_t* npl, int32_t* grid,
+                         int64_t grid_cells, uint32_t epoch, void* stream) {
+  GeomDev d;
+  int rc = make_geom(g, &d);
+  if (rc) return rc;
+  SP_CHECK_ARG(d.mode == SP_PAIR_SUBM, "sp_pairgen_subm_grid needs SP_PAIR_SUBM");
+  SP_CHECK_ARG(indices && grid && (pair_fwd || pair_bwd), "null pointer");
+  const int64_t cells = sp_pairgen_subm_grid_cells(g, n);
+  SP_CHECK_ARG(cells > 0, "pairgen_subm_grid: no dense grid for this geometry (n=%lld)",
+               (long long)n);
+  SP_CHECK_ARG(grid_cells >= cells, "pairgen_subm_grid: grid of %lld cells < %lld",
+               (long long)grid_cells, (long long)cells);
+  SP_CHECK_ARG(epoch >= 1 && epoch <= 255, "pairgen_subm_grid: epoch %u not in 1..255", epoch);
+  hipStream_t s = as_stream(stream);
+  const int mic = (d.kv + 31) / 32;
+  const unsigned blocks = unsigned(cdiv(n, 256));
+  int32_t* cell0 = grid + kGridPad;
+  subm_insert_grid<true><<<blocks, 256, 0, s>>>(indices, int32_t(n), d, cell0, epoch);
+  SP_LAUNCHED();
+  return launch_probe_grid<true>(indices, n, d, cell0, cells - 2 * kGridPad, epoch, pair_fwd,
+                                 pair_bwd, mask_words, mic, npl, s);
 }
 
 int sp_pairgen_conv_build(const sp_geom* g, const int32_t* indices, int64_t n, void* ws,

@@ -92,6 +92,9 @@ _SIGNATURES = {
     "sp_geom_key64": (ctypes.c_int, [_GP]),
     "sp_pairgen_workspace_size": (_SZ, [_GP, _I64]),
     "sp_pairgen_subm": (ctypes.c_int, [_GP, _P, _I64, _P, _P, _P, _P, _SZ, _P]),
+    "sp_pairgen_subm_grid_cells": (_I64, [_GP, _I64]),
+    "sp_pairgen_subm_grid": (ctypes.c_int, [_GP, _P, _I64, _P, _P, _P, _P, _P, _I64,
+                                            ctypes.c_uint32, _P]),
     "sp_pairgen_conv_build": (ctypes.c_int, [_GP, _P, _I64, _P, _SZ, ctypes.POINTER(_I64), _P]),
     "sp_pairgen_conv_fill": (ctypes.c_int, [_GP, _P, _I64, _P, _SZ, _I64, _P, _P, _P, _P, _P]),
     "sp_mask_words": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),

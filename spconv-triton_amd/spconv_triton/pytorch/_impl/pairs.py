@@ -111,13 +111,42 @@ def key_is_int64(batch_size, spatial_shape, out_shape, subm) -> bool:
 class _Tables:
     """Raw tables produced by one pair-generation run."""
 
-    def __init__(self, out_inds, pair_fwd, pair_bwd, words_fwd, words_bwd, n_out):
+    def __init__(self, out_inds, pair_fwd, pair_bwd, words_fwd, words_bwd, n_out, npl=None):
         self.out_inds = out_inds
         self.pair_fwd = pair_fwd
         self.pair_bwd = pair_bwd
         self.words_fwd = words_fwd
         self.words_bwd = words_bwd
         self.n_out = n_out
+        self.npl = npl  # zeroed indice_num_per_loc, when the build wrote it
+
+
+#: Dense cell -> row grids kept between subm builds, one per (device, stream):
+#: (grid, epoch of its last build).  A grid is zero-filled when created and
+#: every 255 builds; in between, each build stamps its cells with a new epoch
+#: (``sp_pairgen_subm_grid``), so no build clears it.
+_GRIDS: dict = {}
+
+
+def _subm_grid(device: torch.device, cells: int):
+    """(grid, epoch) for the next subm build on the current stream of ``device``."""
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    grid, epoch = _GRIDS.get(key, (None, 255))
+    if grid is None or grid.numel() < cells:
+        grid = torch.empty((cells,), dtype=torch.int32, device=device)
+        epoch = 255
+    if epoch >= 255:
+        grid.zero_()
+        epoch = 0
+    epoch += 1
+    _GRIDS[key] = (grid, epoch)
+    return grid, epoch
+
+
+def release_pairgen_grids() -> None:
+    """Drop the kept subm lookup grids (the next build allocates again)."""
+    _GRIDS.clear()
 
 
 def _generate(indices, batch_size, spatial_shape, ksize, stride, padding, dilation, out_padding,
@@ -134,16 +163,28 @@ def _generate(indices, batch_size, spatial_shape, ksize, stride, padding, dilati
               dilation)
     L = _lib.lib()
     stream = _lib.stream_of(device)
-    ws = _lib.workspace(L.sp_pairgen_workspace_size(g, N), device)
     i32 = dict(dtype=torch.int32, device=device)
     if subm:
         pf = torch.empty((kv, N), **i32) if want_fwd else None
         pb = torch.empty((kv, N), **i32) if want_bwd else None
         words = torch.empty((N, mic), **i32) if want_words_fwd else None
+        cells = L.sp_pairgen_subm_grid_cells(g, N)
+        if cells > 0 and not torch.cuda.is_current_stream_capturing():
+            # a grid kept between builds (a graph replays its kernels with the
+            # epoch it was captured with, so captured builds clear their own)
+            grid, epoch = _subm_grid(device, cells)
+            npl = torch.empty((kv,), **i32)
+            _lib.check(L.sp_pairgen_subm_grid(g, _lib.ptr(idx), N, _lib.ptr(pf), _lib.ptr(pb),
+                                              _lib.ptr(words), _lib.ptr(npl), _lib.ptr(grid),
+                                              grid.numel(), epoch, stream),
+                       "sp_pairgen_subm_grid")
+            return _Tables(indices, pf, pb, words, None, N, npl)
+        ws = _lib.workspace(L.sp_pairgen_workspace_size(g, N), device)
         _lib.check(L.sp_pairgen_subm(g, _lib.ptr(idx), N, _lib.ptr(pf), _lib.ptr(pb),
                                      _lib.ptr(words), _lib.ptr(ws), ws.numel(), stream),
                    "sp_pairgen_subm")
         return _Tables(indices, pf, pb, words, None, N)
+    ws = _lib.workspace(L.sp_pairgen_workspace_size(g, N), device)
     n_out = ctypes.c_int64(0)
     _lib.check(L.sp_pairgen_conv_build(g, _lib.ptr(idx), N, _lib.ptr(ws), ws.numel(), n_out,
                                        stream), "sp_pairgen_conv_build")
@@ -295,7 +336,7 @@ def igemm_rulebook(indices, batch_size, spatial_shape, ksize, stride, padding, d
                   want_words_fwd=subm, want_words_bwd=need_bwd and not subm,
                   num_out_act_bound=bound)
     device = t.pair_fwd.device
-    npl = torch.zeros((kv,), dtype=torch.int32, device=device)
+    npl = t.npl if t.npl is not None else torch.zeros((kv,), dtype=torch.int32, device=device)
     masks = split_masks(kv, is_mask_split)
     # t.words_bwd exists for a regular/transposed training rulebook only
     deferred = DeferredMaskSplits(t.words_fwd, t.pair_fwd, t.words_bwd, kv, masks, do_sort)

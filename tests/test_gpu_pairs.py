@@ -106,7 +106,7 @@ def _subm_uses_dense_grid(batch, shape, ks, n):
 
     g = _lib.make_geom(_lib.SP_PAIR_SUBM, batch, shape, shape, ks, [1] * len(shape),
                        [0] * len(shape), [1] * len(shape))
-    return _lib.lib().sp_pairgen_workspace_size(g, n) == batch * int(np.prod(shape)) * 4
+    return _lib.lib().sp_pairgen_workspace_size(g, n) == (batch * int(np.prod(shape)) + 8) * 4
 
 
 SUBM_GEOMS = [i for i, g in enumerate(GEOMS) if g[6]]
@@ -573,3 +573,122 @@ def test_unsorted_masks_bit_exact(gi):
         _compare_igemm(res, exp, t, subm, True)
         for ar in res[6]:
             assert torch.equal(ar, torch.arange(ar.numel(), dtype=torch.int32, device=DEV))
+
+
+def _subm_tables_direct(idx_t, batch, shape, ks, kept_grid):
+    """pair_fwd / pair_bwd / mask words of a subm build through one of the
+    two C-ABI entry points: the cleared-workspace build (sp_pairgen_subm) or
+    the kept-grid build (sp_pairgen_subm_grid, through the package's grid)."""
+    from spconv_triton.pytorch._impl import _lib, pairs as P
+
+    L = _lib.lib()
+    nd = len(shape)
+    n = idx_t.shape[0]
+    kv = int(np.prod(ks))
+    g = _lib.make_geom(_lib.SP_PAIR_SUBM, batch, shape, shape, ks, [1] * nd,
+                       [k // 2 for k in ks], [1] * nd)
+    pf = torch.empty((kv, n), dtype=torch.int32, device=DEV)
+    pb = torch.empty((kv, n), dtype=torch.int32, device=DEV)
+    words = torch.empty((n, (kv + 31) // 32), dtype=torch.int32, device=DEV)
+    stream = _lib.stream_of(torch.device(DEV))
+    if kept_grid:
+        cells = L.sp_pairgen_subm_grid_cells(g, n)
+        assert cells > 0
+        grid, epoch = P._subm_grid(torch.device(DEV), cells)
+        npl = torch.full((kv,), 7, dtype=torch.int32, device=DEV)
+        _lib.check(L.sp_pairgen_subm_grid(g, _lib.ptr(idx_t), n, _lib.ptr(pf), _lib.ptr(pb),
+                                          _lib.ptr(words), _lib.ptr(npl), _lib.ptr(grid),
+                                          grid.numel(), epoch, stream), "sp_pairgen_subm_grid")
+        assert int(npl.abs().sum()) == 0, "npl must come back zeroed"
+    else:
+        ws = _lib.workspace(L.sp_pairgen_workspace_size(g, n), torch.device(DEV))
+        _lib.check(L.sp_pairgen_subm(g, _lib.ptr(idx_t), n, _lib.ptr(pf), _lib.ptr(pb),
+                                     _lib.ptr(words), _lib.ptr(ws), ws.numel(), stream),
+                   "sp_pairgen_subm")
+    return pf, pb, words
+
+
+def test_subm_kept_grid_across_builds_and_epoch_wrap():
+    """The kept grid is never cleared between builds: cells stamped by earlier
+    builds -- of other geometries too -- must read as empty.  Builds of two
+    clouds alternate across the epoch wrap (epoch 255, then a refill and
+    epoch 1); every build matches the oracle and the cleared-workspace path."""
+    from spconv_triton.pytorch._impl import pairs as P
+
+    rng = np.random.default_rng(77)
+    clouds = []
+    for shape in ([30, 16, 26], [24, 20, 22]):  # the larger grid first: it is kept
+        idx = rand_indices(rng, 2, shape, int(np.prod(shape)) // 4)
+        clouds.append((shape, idx, torch.from_numpy(idx).to(DEV)))
+    P.release_pairgen_grids()
+    key = (torch.device(DEV).index, torch.cuda.current_stream(torch.device(DEV)).cuda_stream)
+    seen = []
+    for step in range(8):
+        if step == 3:  # jump to the end of the epoch range
+            grid, _ = P._GRIDS[key]
+            P._GRIDS[key] = (grid, 253)
+        shape, idx, t = clouds[step % 2]
+        pf, pb, words = _subm_tables_direct(t, 2, shape, [3, 3, 3], True)
+        seen.append(P._GRIDS[key][1])
+        exp = orc.igemm_pairs(idx, 2, shape, [3] * 3, [1] * 3, [1] * 3, [1] * 3, [0] * 3, True,
+                              False, True)
+        _eq(pf, exp[2], f"pair_fwd build {step}")
+        _eq(pb, exp[3], f"pair_bwd build {step}")
+        rf, rb, rw = _subm_tables_direct(t, 2, shape, [3, 3, 3], False)
+        assert torch.equal(pf, rf) and torch.equal(pb, rb) and torch.equal(words, rw)
+    assert seen == [1, 2, 3, 254, 255, 1, 2, 3], seen
+
+
+def test_subm_duplicate_coordinates_keep_smallest_row_both_paths():
+    """Duplicate coordinates are outside the reference's contract; both subm
+    builds resolve a cell held by several rows to its smallest row."""
+    rng = np.random.default_rng(5)
+    shape = [16, 16, 16]
+    idx = rand_indices(rng, 1, shape, 600)
+    dup = idx[rng.choice(idx.shape[0], 80, replace=False)]
+    idx = np.concatenate([idx, dup], 0)[rng.permutation(idx.shape[0] + 80)].astype(np.int32)
+    t = torch.from_numpy(idx).to(DEV)
+    kept = _subm_tables_direct(t, 1, shape, [3, 3, 3], True)
+    cleared = _subm_tables_direct(t, 1, shape, [3, 3, 3], False)
+    for a, b in zip(kept, cleared):
+        assert torch.equal(a, b)
+    # the centre offset of a duplicated cell names the cell's smallest row
+    keys = np.ravel_multi_index(idx[:, 1:].T, shape)
+    first = {}
+    for r, k in enumerate(keys):
+        first.setdefault(k, r)
+    centre = kept[0][13].cpu().numpy()
+    assert all(centre[r] == first[k] for r, k in enumerate(keys))
+
+
+def test_subm_build_inside_graph_capture_replays():
+    """A subm rulebook built while the stream is captured takes the clearing
+    path (a replay reruns the capture's kernels with their arguments); replays
+    equal the eager build."""
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+
+    rng = np.random.default_rng(8)
+    shape = [20, 20, 20]
+    idx = torch.from_numpy(rand_indices(rng, 1, shape, 1500)).to(DEV)
+
+    def build():
+        return ops.get_indice_pairs_implicit_gemm(idx, 1, shape, ConvAlgo.MaskImplicitGemm,
+                                                  [3] * 3, [1] * 3, [1] * 3, [1] * 3, [0] * 3,
+                                                  True, is_train=True)
+
+    eager = build()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        build()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cap = build()
+    for _ in range(3):
+        cap[2].fill_(-5)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(cap[2], eager[2]) and torch.equal(cap[3], eager[3])
+        build()  # eager work between replays
