@@ -278,6 +278,68 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool 
     return variant
 
 
+#: Key order for planned GEMMs: a table whose natural 256-row tiles mostly
+#: overflow LDS (more than KEY_ORDER_MIN_OVERFLOW of its tiles reference more
+#: distinct source rows than the plan can stage: rows in no spatial order,
+#: e.g. a random permutation of the voxels) takes its rows sorted by their
+#: linear coordinate key instead, where a tile's rows are spatial neighbours.
+#: The table's rows' coordinates come from pair generation.
+KEY_ORDER_MIN_OVERFLOW = 0.25
+
+
+def key_order(coords) -> torch.Tensor:
+    """Stable argsort of rows by batch-major linear key (int32 [M]): the rows'
+    coordinates [M, ndim+1], spatial shape and batch size."""
+    from . import pairs as _pairs
+    idx, shape, batch = coords
+    key = idx[:, 0].to(torch.int64)
+    for d, n in enumerate(shape):
+        key = key * int(n) + idx[:, d + 1].to(torch.int64)
+    volume = int(batch)
+    for n in shape:
+        volume *= int(n)
+    bits = max(1, (volume - 1).bit_length())
+    if bits <= 32:
+        words = key.to(torch.int32).view(-1, 1)
+    else:  # two words, the high one most significant
+        words = torch.stack([(key & 0xFFFFFFFF).to(torch.int32), (key >> 32).to(torch.int32)], 1)
+    _, ar = _pairs.sort_mask_words(words.contiguous(), bits, _pairs.split_masks(bits, False), True)
+    return ar[0]
+
+
+def key_order_variant(pairs: torch.Tensor, n_src: int, plan: torch.Tensor):
+    """(order, permuted table, its gather plan) when a planned GEMM on this
+    table should take its rows in key order (see KEY_ORDER_MIN_OVERFLOW), else
+    None.  Decided on the table's second planned GEMM, like the mask order
+    (row_order_variant): the first call launches nothing, the second reads the
+    plan's overflow count back (one synchronization) and, when most tiles
+    overflow, sorts the rows by key, permutes the table and plans it.  The
+    outcome is memoised on the table tensor.  Calls made while the stream is
+    being captured into a graph use a settled order but never advance the
+    decision."""
+    coords = getattr(pairs, "_spconv_triton_rowcoords", None)
+    if coords is None or plan is None or coords[0].shape[0] != pairs.shape[1]:
+        return None
+    stamp = (int(n_src), pairs._version, pairs.data_ptr())
+    cached = getattr(pairs, "_spconv_triton_keyorder", None)
+    step = cached[1] if cached is not None and cached[0] == stamp else "start"
+    if isinstance(step, tuple):
+        return step
+    if step == "natural" or torch.cuda.is_current_stream_capturing():
+        return None
+    if step == "start":
+        pairs._spconv_triton_keyorder = (stamp, "seen")
+        return None
+    tiles = (pairs.shape[1] + 255) // 256
+    variant = None
+    if plan_overflow_count(plan) > KEY_ORDER_MIN_OVERFLOW * tiles:
+        order = key_order(coords)
+        perm = permute_table(pairs, order)
+        variant = (order, perm, gather_plan(perm, n_src))
+    pairs._spconv_triton_keyorder = (stamp, variant if variant is not None else "natural")
+    return variant
+
+
 def plan_overflow_count(plan: torch.Tensor) -> int:
     """Number of tiles of a plan whose distinct rows do not fit in LDS (the
     plan's first int32; reading it synchronizes)."""
@@ -297,6 +359,10 @@ def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: 
     variant = row_order_variant(pairs, a.shape[0], K * C, use_plan)
     if split:  # the GEMM's reduction dimension is tripled
         K, C = (3 * K, C) if transpose else (K, 3 * C)
+    if variant is None:
+        plan = gather_plan(pairs, a.shape[0]) if use_plan else None
+        if plan is not None:
+            variant = key_order_variant(pairs, a.shape[0], plan)
     if variant is not None:
         order, perm, plan = variant
         _lib.check(L.sp_conv_gemm_ordered(
@@ -305,7 +371,6 @@ def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: 
             _lib.ptr(plan), 0 if plan is None else plan.numel(), _lib.ptr(out),
             _lib.dtype_code(out.dtype), _lib.stream_of(a.device)), "sp_conv_gemm_ordered")
         return
-    plan = gather_plan(pairs, a.shape[0]) if use_plan else None
     if plan is not None:
         # the planned kernel skips empty offsets itself: mask tables are not needed
         _lib.check(L.sp_conv_gemm_planned(

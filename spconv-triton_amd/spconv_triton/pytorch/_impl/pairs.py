@@ -149,6 +149,14 @@ def release_pairgen_grids() -> None:
     _GRIDS.clear()
 
 
+def _attach_coords(table, coords, shape, batch) -> None:
+    """Keep the coordinates of a gather table's rows on the table (rows of
+    ``coords`` [M, ndim+1] int32 in ``shape``, ``batch`` samples): the GEMM
+    may reorder rows by their linear key (``gemm.key_order_variant``)."""
+    if table is not None and table.numel() > 0 and coords is not None:
+        table._spconv_triton_rowcoords = (coords, tuple(int(v) for v in shape), int(batch))
+
+
 def _generate(indices, batch_size, spatial_shape, ksize, stride, padding, dilation, out_padding,
               subm, transpose, want_fwd, want_bwd, want_words_fwd, want_words_bwd,
               num_out_act_bound=-1) -> _Tables:
@@ -178,12 +186,15 @@ def _generate(indices, batch_size, spatial_shape, ksize, stride, padding, dilati
                                               _lib.ptr(words), _lib.ptr(npl), _lib.ptr(grid),
                                               grid.numel(), epoch, stream),
                        "sp_pairgen_subm_grid")
-            return _Tables(indices, pf, pb, words, None, N, npl)
-        ws = _lib.workspace(L.sp_pairgen_workspace_size(g, N), device)
-        _lib.check(L.sp_pairgen_subm(g, _lib.ptr(idx), N, _lib.ptr(pf), _lib.ptr(pb),
-                                     _lib.ptr(words), _lib.ptr(ws), ws.numel(), stream),
-                   "sp_pairgen_subm")
-        return _Tables(indices, pf, pb, words, None, N)
+        else:
+            npl = None
+            ws = _lib.workspace(L.sp_pairgen_workspace_size(g, N), device)
+            _lib.check(L.sp_pairgen_subm(g, _lib.ptr(idx), N, _lib.ptr(pf), _lib.ptr(pb),
+                                         _lib.ptr(words), _lib.ptr(ws), ws.numel(), stream),
+                       "sp_pairgen_subm")
+        _attach_coords(pf, idx, spatial_shape, batch_size)
+        _attach_coords(pb, idx, spatial_shape, batch_size)
+        return _Tables(indices, pf, pb, words, None, N, npl)
     ws = _lib.workspace(L.sp_pairgen_workspace_size(g, N), device)
     n_out = ctypes.c_int64(0)
     _lib.check(L.sp_pairgen_conv_build(g, _lib.ptr(idx), N, _lib.ptr(ws), ws.numel(), n_out,
@@ -205,6 +216,8 @@ def _generate(indices, batch_size, spatial_shape, ksize, stride, padding, dilati
     words_fwd = None
     if want_words_fwd:
         words_fwd = mask_words(pf)
+    _attach_coords(pf, out_inds, out_shape, batch_size)
+    _attach_coords(pb, idx, spatial_shape, batch_size)
     return _Tables(out_inds, pf, pb, words_fwd, words_bwd, n_out)
 
 
@@ -265,6 +278,12 @@ def native_pairs(indices, batch_size, spatial_shape, ksize, stride, padding, dil
     _lib.check(L.sp_compact_table(_lib.ptr(pb), kv, N, _lib.ptr(pair[0]), _lib.ptr(pair[1]), None,
                                   _lib.ptr(npl), (kv // 2) if subm else kv, _lib.ptr(ws),
                                   ws.numel(), _lib.stream_of(device)), "sp_compact_table")
+    out_shape = _check_and_shape(indices, spatial_shape, ksize, stride, padding, dilation,
+                                 out_padding, subm, transpose)
+    pair._spconv_triton_rowcoords = {
+        "in": (_prepare_indices(indices), tuple(spatial_shape), int(batch_size)),
+        "out": (t.out_inds if not subm else _prepare_indices(indices), tuple(out_shape),
+                int(batch_size))}
     return t.out_inds, pair, npl
 
 
@@ -380,5 +399,12 @@ def native_pair_to_tables(pair: torch.Tensor, indice_pair_num, n_in: int, n_out:
         _lib.check(_lib.lib().sp_native_to_tables(
             _lib.ptr(pc), kv, n_pairs, int(bool(inverse)), int(n_in), int(n_out), _lib.ptr(pf),
             _lib.ptr(pb) if need_bwd else None, _lib.stream_of(device)), "sp_native_to_tables")
+        coords = getattr(pair, "_spconv_triton_rowcoords", None)
+        if coords is not None:
+            fwd_rows, bwd_rows = (coords["in"], coords["out"]) if inverse else \
+                (coords["out"], coords["in"])
+            _attach_coords(pf, *fwd_rows)
+            if need_bwd:
+                _attach_coords(pb, *bwd_rows)
         cache[key] = (pf, pb)
     return pf, pb

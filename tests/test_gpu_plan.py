@@ -515,3 +515,47 @@ def test_graph_replay_reads_updated_weights(dtype):
         torch.cuda.synchronize()
         assert torch.equal(y, ey), f"replay {step}: forward used stale weights"
         assert torch.equal(dx, edx), f"replay {step}: dgrad used stale weights"
+
+
+def test_key_order_for_unordered_rows():
+    """Rows in no spatial order (a random permutation of a surface cloud) make
+    every natural tile overflow LDS; the table's second planned GEMM sorts its
+    rows by linear key and reruns through the ordered kernel.  Results stay
+    bit-identical: to the first (natural-order) call, to the unplanned kernel,
+    and, row for row, to the same layer on the sorted cloud."""
+    import bench_data
+    from spconv_triton.pytorch._impl import gemm
+
+    sorted_idx = bench_data.surface_cloud(120_000, 192, seed=4)
+    perm = np.random.default_rng(4).permutation(sorted_idx.shape[0])
+    idx = np.ascontiguousarray(sorted_idx[perm])
+    n = idx.shape[0]
+    pf = _tables(idx, 1, [192] * 3, [3] * 3, [1] * 3, [1] * 3, True)[2]
+    pf_sorted = _tables(sorted_idx, 1, [192] * 3, [3] * 3, [1] * 3, [1] * 3, True)[2]
+    torch.manual_seed(5)
+    x_sorted = torch.randn(n, 64, device=DEV).half()
+    x = x_sorted[torch.from_numpy(perm).to(DEV)].contiguous()
+    w = (torch.randn(64, 27, 64, device=DEV) / np.sqrt(27 * 64)).half()
+    b = torch.randn(64, device=DEV).half()
+    first = gemm.conv_forward(x, w, pf, n, b)
+    assert pf._spconv_triton_keyorder[1] == "seen"
+    second = gemm.conv_forward(x, w, pf, n, b)
+    variant = pf._spconv_triton_keyorder[1]
+    assert isinstance(variant, tuple), "mostly overflowing tiles must settle the key order"
+    order = variant[0].cpu().numpy()
+    keys = np.ravel_multi_index(idx[:, 1:].T, [192] * 3)
+    assert np.array_equal(keys[order], np.sort(keys))
+    assert gemm.plan_overflow_count(variant[2]) == 0
+    assert torch.equal(first, second)
+    prev = gemm.USE_GATHER_PLAN
+    gemm.USE_GATHER_PLAN = False
+    try:
+        direct = gemm.conv_forward(x, w, pf, n, b)
+    finally:
+        gemm.USE_GATHER_PLAN = prev
+    assert torch.equal(second, direct)
+    ref = gemm.conv_forward(x_sorted, w, pf_sorted, n, b)
+    assert torch.equal(second, ref[torch.from_numpy(perm).to(DEV)])
+    # the sorted cloud's own table keeps its natural order
+    gemm.conv_forward(x_sorted, w, pf_sorted, n, b)
+    assert pf_sorted._spconv_triton_keyorder[1] == "natural"
