@@ -120,37 +120,42 @@ __device__ __forceinline__ float split_part(float v, bool lo) {
 //   forward: n = output channel (K), r = input channel (C)
 //   dgrad:   n = input channel (C),  r = output channel (K)
 // ---------------------------------------------------------------------------
+// One launch writes both parts of a packed weight: the relaid B, one 16-byte
+// piece (V elements) per thread, and, from its first N threads, the fp32 bias
+// (zeros without one).  The packed buffer stays below 1 GiB, so indices fit
+// in 32 bits.
 template <typename T>
-__global__ void relayout_weight(const void* __restrict__ w, int w_dtype, int64_t K, int64_t kv,
-                                int64_t C, int transpose, int N, int R, int Rp, int split_r,
-                                T* __restrict__ bt) {
+__global__ void relayout_weight(const void* __restrict__ w, int w_dtype, int K, int kv, int C,
+                                int transpose, int N, int R, int Rp, int split_r,
+                                T* __restrict__ bt, const void* __restrict__ bias,
+                                float* __restrict__ bias_out) {
   constexpr int V = Mfma<T>::V;
-  const int64_t total = kv * int64_t(Rp) * N;
-  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const int e = int(i % V);
-  int64_t t = i / V;
-  const int n = int(t % N);
-  t /= N;
-  const int rv = int(t % (Rp / V));
-  const int64_t k = t / (Rp / V);
-  int r = rv * V + e;
-  float v = 0.f;
-  if (r < R) {
-    // split_r > 0: the reduction axis holds [hi | lo | hi] of the weight's
-    // own split_r-long axis (bf16 parts of an fp32 weight, see split_part)
-    const int part = split_r ? r / split_r : 0;
-    if (split_r) r -= part * split_r;
-    const int64_t src = transpose ? (int64_t(r) * kv + k) * C + n : (int64_t(n) * kv + k) * C + r;
-    v = load_any(w, w_dtype, src);
-    if (split_r) v = split_part(v, part == 1);
+  const int pieces = kv * (Rp / V) * N;
+  const int i = int(blockIdx.x) * int(blockDim.x) + int(threadIdx.x);
+  if (i < N) bias_out[i] = bias ? load_any(bias, w_dtype, i) : 0.f;
+  if (i >= pieces) return;
+  const int n = i % N;
+  const int t = i / N;
+  const int rv = t % (Rp / V);
+  const int k = t / (Rp / V);
+  T vals[V];
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    int r = rv * V + e;
+    float v = 0.f;
+    if (r < R) {
+      // split_r > 0: the reduction axis holds [hi | lo | hi] of the weight's
+      // own split_r-long axis (bf16 parts of an fp32 weight, see split_part)
+      const int part = split_r ? r / split_r : 0;
+      if (split_r) r -= part * split_r;
+      const int64_t src =
+          transpose ? (int64_t(r) * kv + k) * C + n : (int64_t(n) * kv + k) * C + r;
+      v = load_any(w, w_dtype, src);
+      if (split_r) v = split_part(v, part == 1);
+    }
+    vals[e] = from_f32<T>(v);
   }
-  bt[i] = from_f32<T>(v);
-}
-
-__global__ void bias_to_f32(const void* __restrict__ b, int dtype, int n, float* __restrict__ out) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) out[i] = b ? load_any(b, dtype, i) : 0.f;
+  *reinterpret_cast<uint4*>(bt + int64_t(i) * V) = __builtin_bit_cast(uint4, vals);
 }
 
 // ---------------------------------------------------------------------------
@@ -462,29 +467,35 @@ static int pack_weight(const void* w, int w_dtype, const void* bias, int64_t K, 
                "pack: bad sizes K=%lld kv=%lld C=%lld", (long long)K, (long long)kv, (long long)C);
   SP_CHECK_ARG(w && packed, "pack: null pointer");
   const Packed p = packed_layout(K, kv, C, dtype, transpose);
-  const int64_t tot = kv * int64_t(p.Rp) * p.N;
-  const unsigned rb = unsigned(cdiv(tot, 256));
+  SP_CHECK_ARG(p.bt_bytes < kMaxBtBytes, "pack: packed weights of %zu B exceed 1 GiB", p.bt_bytes);
+  const int64_t tot = kv * int64_t(p.Rp / vec_of(dtype)) * p.N;  // 16-byte pieces
+  const unsigned rb = unsigned(cdiv(tot > p.N ? tot : p.N, 256));
   char* base = static_cast<char*>(packed);
+  float* bias_out = reinterpret_cast<float*>(base + p.bias_off);
   switch (dtype) {
     case SP_F16:
-      relayout_weight<_Float16><<<rb, 256, 0, s>>>(w, w_dtype, K, kv, C, transpose, p.N, p.R,
-                                                   p.Rp, 0, reinterpret_cast<_Float16*>(base));
+      relayout_weight<_Float16><<<rb, 256, 0, s>>>(w, w_dtype, int(K), int(kv), int(C), transpose,
+                                                   p.N, p.R, p.Rp, 0, reinterpret_cast<_Float16*>(base),
+                                                   bias, bias_out);
       break;
     case SP_BF16:
-      relayout_weight<__bf16><<<rb, 256, 0, s>>>(w, w_dtype, K, kv, C, transpose, p.N, p.R, p.Rp,
-                                                 0, reinterpret_cast<__bf16*>(base));
+      relayout_weight<__bf16><<<rb, 256, 0, s>>>(w, w_dtype, int(K), int(kv), int(C), transpose,
+                                                 p.N, p.R, p.Rp,
+                                                 0, reinterpret_cast<__bf16*>(base), bias,
+                                                 bias_out);
       break;
     case SP_BF16X3:
-      relayout_weight<__bf16><<<rb, 256, 0, s>>>(w, w_dtype, K, kv, C, transpose, p.N, p.R, p.Rp,
-                                                 p.R / 3, reinterpret_cast<__bf16*>(base));
+      relayout_weight<__bf16><<<rb, 256, 0, s>>>(w, w_dtype, int(K), int(kv), int(C), transpose,
+                                                 p.N, p.R, p.Rp,
+                                                 p.R / 3, reinterpret_cast<__bf16*>(base), bias,
+                                                 bias_out);
       break;
     default:
-      relayout_weight<float><<<rb, 256, 0, s>>>(w, w_dtype, K, kv, C, transpose, p.N, p.R, p.Rp,
-                                                0, reinterpret_cast<float*>(base));
+      relayout_weight<float><<<rb, 256, 0, s>>>(w, w_dtype, int(K), int(kv), int(C), transpose,
+                                                p.N, p.R, p.Rp,
+                                                0, reinterpret_cast<float*>(base), bias,
+                                                bias_out);
   }
-  SP_LAUNCHED();
-  bias_to_f32<<<unsigned(cdiv(p.N, 256)), 256, 0, s>>>(bias, w_dtype, p.N,
-                                                      reinterpret_cast<float*>(base + p.bias_off));
   SP_LAUNCHED();
   return SP_OK;
 }

@@ -251,7 +251,16 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool 
     cached = getattr(pairs, "_spconv_triton_order", None)
     step = cached[1] if cached is not None and cached[0] == stamp else "start"
     if isinstance(step, tuple):
-        return step  # a settled mask order serves every layer on the table
+        # a settled mask order serves every layer on the table, each with or
+        # without the permuted table's gather plan as the call asks (built on
+        # the first call that wants it)
+        order, perm, plan = step
+        if not (plan_ok and kv <= _PLAN_MAX_KV):
+            return step if plan is None else (order, perm, None)
+        if plan is None and not torch.cuda.is_current_stream_capturing():
+            step = (order, perm, gather_plan(perm, n_src))
+            pairs._spconv_triton_order = (stamp, step)
+        return step
     if step == "natural" or (mode == "auto" and (work < ORDER_MIN_WORK or kv > _STATS_MAX_KV)):
         return None  # narrow layers never start the decision
     if torch.cuda.is_current_stream_capturing():
