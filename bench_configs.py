@@ -21,7 +21,11 @@ weights, and prints one JSON object per configuration:
   surface voxels in 256^3, rulebooks rebuilt every pass (config 2);
 * ``lidar_c256``: SubMConv3d 256 -> 256 on a 50k-voxel LiDAR cloud, rulebook
   cached, in fp16, IEEE fp32 and fp32 with SPCONV_ALLOW_TF32 (split-bf16
-  products), with the pairs per row and the matrix-core utilisation.
+  products), with the pairs per row and the matrix-core utilisation;
+* ``ref_c256``: the layer class of the reference's published plots (K3, C256,
+  50k voxels in [41, 1600, 1408], batch 1) on uniform voxels: submanifold with
+  the rulebook cached, strided and transposed with pair generation, in fp16,
+  fp32 and TF32-equivalent.
 
 Usage: ``python bench_configs.py [--config NAME ...] [--reps R]``.
 """
@@ -311,9 +315,74 @@ def cfg_lidar_c256(reps):
     return out
 
 
+def _event_ms(fn, n):
+    """Mean ms per call of ``fn`` over ``n`` back-to-back calls, between two
+    events (the calls that sync the host, such as pair generation with an
+    output-size readback, are included as the reference's timings include
+    them)."""
+    for _ in range(5):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
+def cfg_ref_c256(reps):
+    """The layer class of the reference's published plots (K3, C256, batch 1,
+    ~50k voxels in 41 x 1600 x 1408): submanifold with the rulebook cached,
+    strided (k3 s2 p1) and transposed (k3 s2) with the rulebook rebuilt every
+    pass.  The reference's harness and cloud are not published; the voxels here
+    are uniform in the grid."""
+    import spconv_triton.pytorch as spconv
+    from bench_data import uniform_cloud
+    from spconv_triton import constants
+
+    shape = [41, 1600, 1408]
+    idx = uniform_cloud(50000, shape, seed=0)
+    it = torch.from_numpy(idx).to(DEV)
+    n = int(idx.shape[0])
+    out = {"voxels": n}
+    for name, dtype, tf32 in (("fp16", torch.float16, False), ("fp32", torch.float32, False),
+                              ("tf32", torch.float32, True)):
+        torch.manual_seed(0)
+        feats = torch.randn(n, 256, device=DEV).to(dtype)
+        subm = spconv.SubMConv3d(256, 256, 3, padding=1, bias=False, indice_key="k")
+        down = spconv.SparseConv3d(256, 256, 3, stride=2, padding=1, bias=False)
+        up = spconv.SparseConvTranspose3d(256, 256, 3, stride=2, bias=False)
+        subm, down, up = (m.to(DEV).to(dtype).eval() for m in (subm, down, up))
+        prev = constants.SPCONV_ALLOW_TF32
+        constants.SPCONV_ALLOW_TF32 = tf32
+        try:
+            with torch.no_grad():
+                y = subm(spconv.SparseConvTensor(feats, it, shape, 1))
+                pairs = int((y.indice_dict["k"].pair_fwd >= 0).sum().item())
+                xc = spconv.SparseConvTensor(feats, it, shape, 1, indice_dict=y.indice_dict)
+                k = 10 * reps
+                res = {"subm_ms": _event_ms(lambda: subm(xc), k),
+                       "sparse_s2_ms": _event_ms(
+                           lambda: down(spconv.SparseConvTensor(feats, it, shape, 1)), k),
+                       "transpose_s2_ms": _event_ms(
+                           lambda: up(spconv.SparseConvTensor(feats, it, shape, 1)), k)}
+                n_up = int(up(spconv.SparseConvTensor(feats, it, shape, 1)).features.shape[0])
+        finally:
+            constants.SPCONV_ALLOW_TF32 = prev
+        out[name] = {key: round(v, 4) for key, v in res.items()}
+    out["subm_pairs_per_row"] = round(pairs / n, 3)
+    out["transpose_out_voxels"] = n_up
+    out["what"] = ("K3 C256 batch 1, 50k uniform voxels in 41x1600x1408: subm forward with the "
+                   "rulebook cached; strided and transposed forwards with pair generation, "
+                   "mean of events")
+    return out
+
+
 CONFIGS = {"encoder": cfg_encoder, "resunet": cfg_resunet, "subm4d": cfg_subm4d,
            "wide": cfg_wide, "config1": cfg_config1, "quickstart": cfg_quickstart,
-           "lidar_c256": cfg_lidar_c256}
+           "lidar_c256": cfg_lidar_c256, "ref_c256": cfg_ref_c256}
 
 
 def main() -> int:

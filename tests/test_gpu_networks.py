@@ -320,6 +320,52 @@ def _l2_check(name, actual, expected, max_rel_l2, min_cos):
         f"(bound {min_cos})")
 
 
+# Measured (relative L2, cosine) of every fp16-autocast ResUNet gradient
+# against the fp64 oracle on MI355X (the kernels are deterministic, so these
+# repeat); the test bounds each at 1.5x its own error.
+FP16_GRAD_ERRORS = {
+    "grad input": (0.0403, 0.999186),
+    "head weight grad": (0.000308, 1.000000),
+    "head bias grad": (0.000211, 1.000000),
+    "stem.0 grad": (0.0347, 0.999397),
+    "stem.1 grad": (0.0274, 0.999632),
+    "stem.2 grad": (0.0366, 0.999328),
+    "e1.0 grad": (0.0483, 0.998834),
+    "e1.1 grad": (0.0474, 0.998884),
+    "e1.2 grad": (0.0495, 0.998868),
+    "e1.3 grad": (0.0496, 0.998768),
+    "e1.4 grad": (0.0525, 0.998623),
+    "e1.5 grad": (0.0452, 0.998987),
+    "e2.0 grad": (0.0547, 0.998507),
+    "e2.1 grad": (0.0571, 0.998383),
+    "e2.2 grad": (0.0494, 0.998787),
+    "e3.0 grad": (0.0558, 0.998443),
+    "e3.1 grad": (0.059, 0.998269),
+    "e3.2 grad": (0.0575, 0.998393),
+    "e3.3 grad": (0.0553, 0.998468),
+    "e3.4 grad": (0.062, 0.998089),
+    "e3.5 grad": (0.0517, 0.998675),
+    "u3.0 grad": (0.0544, 0.998519),
+    "u3.1 grad": (0.0509, 0.998724),
+    "u3.2 grad": (0.0477, 0.998866),
+    "m2.0 grad": (0.0505, 0.998725),
+    "m2.1 grad": (0.047, 0.998899),
+    "m2.2 grad": (0.0406, 0.999176),
+    "u2.0 grad": (0.049, 0.998800),
+    "u2.1 grad": (0.0477, 0.998864),
+    "u2.2 grad": (0.0493, 0.998860),
+    "m1.0 grad": (0.0428, 0.999084),
+    "m1.1 grad": (0.0296, 0.999573),
+    "m1.2 grad": (0.0272, 0.999630),
+    "u1.0 grad": (0.0313, 0.999510),
+    "u1.1 grad": (0.0121, 0.999933),
+    "u1.2 grad": (0.0246, 0.999701),
+    "m0.0 grad": (0.0142, 0.999900),
+    "m0.1 grad": (0.000244, 1.000000),
+    "m0.2 grad": (0.00224, 0.999998),
+}
+
+
 def test_resunet_training_step_autocast_fp16():
     """The same step under torch.autocast(float16): sparse convolutions take
     fp16 inputs and return fp16 (fp32 accumulation), as the reference's
@@ -329,18 +375,24 @@ def test_resunet_training_step_autocast_fp16():
     (oracle_pipeline.ROUND).
 
     Bounds: loss 1e-4 and logits 5e-3 of the largest reference value.  The
-    gradients are compared by relative L2 error (bound 0.15) and cosine
-    similarity (bound 0.99): fp16 storage alone moves this network's
-    gradients by 1.5-6.7 % in L2 (cosine >= 0.9977) from the fp64 ones --
-    measured on the oracle with and without the rounding -- and by up to 16 %
-    of the largest value element-wise, so element-wise bounds do not apply."""
+    gradients are compared by relative L2 error and cosine similarity, each
+    bounded at 1.5x its measured error (FP16_GRAD_ERRORS: relative L2 2e-4 to
+    6.2e-2): fp16 storage alone moves this network's gradients by 1.5-6.7 % in
+    L2 (cosine >= 0.9977) from the fp64 ones -- measured on the oracle with and
+    without the rounding -- and by up to 16 % of the largest value
+    element-wise, so element-wise bounds do not apply.  One wrong offset in one
+    layer's input gradient moves that layer's and every earlier layer's
+    gradients by far more than half their error again."""
     (loss, loss_o), (lg, lo), grads = _resunet_step(True, loss_scale=4096.0)
     _rel_check("loss", loss, loss_o, 1e-4)
     _rel_check("logits", lg, lo, 5e-3)
     bad = []
+    assert {name for name, _, _ in grads} == set(FP16_GRAD_ERRORS)
     for name, a, e in grads:
+        rel, cos = FP16_GRAD_ERRORS[name]
         try:
-            _l2_check(name, a, e, 0.15, 0.99)
+            # (cosines are recorded to 6 decimals: 1e-6 of slack for the rounding)
+            _l2_check(name, a, e, 1.5 * rel, 1.0 - (1.5 * (1.0 - cos) + 1e-6))
         except AssertionError as exc:
             bad.append(str(exc))
     assert not bad, "\n".join(bad)

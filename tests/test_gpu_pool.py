@@ -47,7 +47,8 @@ GEOMS = [
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16, torch.float64])
 @pytest.mark.parametrize("gi", range(len(GEOMS)))
 @pytest.mark.parametrize("ties", [False, True])
-def test_maxpool_bit_exact(gi, dtype, ties):
+@pytest.mark.parametrize("C", [24, 5])  # whole 16-byte pieces (vector kernels) or not
+def test_maxpool_bit_exact(gi, dtype, ties, C):
     from spconv_triton.pytorch._impl import pool
 
     ks, st, pad, dil, subm = GEOMS[gi]
@@ -55,7 +56,7 @@ def test_maxpool_bit_exact(gi, dtype, ties):
     idx = rand_indices(rng, 2, [22] * 3, 2500)
     res = _tables(idx, 2, [22] * 3, ks, st, pad, dil, subm)
     pf, pb = res[2], res[3]
-    x = torch.randn(idx.shape[0], 24)
+    x = torch.randn(idx.shape[0], C)
     if ties:
         x = torch.round(x * 2) / 2  # many equal values: equality routing matters
     x = x.to(DEV, dtype)
@@ -65,7 +66,7 @@ def test_maxpool_bit_exact(gi, dtype, ties):
     ref = orc.maxpool_fwd(xn, pf.cpu().numpy())
     np.testing.assert_array_equal(out.float().cpu().numpy() if dtype == torch.bfloat16
                                   else out.cpu().numpy(), ref.astype(xn.dtype))
-    g = torch.randn(n_out, 24).to(DEV, dtype)
+    g = torch.randn(n_out, C).to(DEV, dtype)
     dx = pool.maxpool_backward(x, out, g, pb)
     gn = g.float().cpu().numpy() if dtype == torch.bfloat16 else g.cpu().numpy()
     on = out.float().cpu().numpy() if dtype == torch.bfloat16 else out.cpu().numpy()
@@ -92,7 +93,8 @@ def test_maxpool_zero_init_all_negative():
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.float16])
 @pytest.mark.parametrize("gi", [0, 1, 2])
-def test_avgpool_bit_exact(gi, dtype):
+@pytest.mark.parametrize("C", [16, 3])
+def test_avgpool_bit_exact(gi, dtype, C):
     from spconv_triton.pytorch._impl import pool
 
     ks, st, pad, dil, subm = GEOMS[gi]
@@ -100,13 +102,58 @@ def test_avgpool_bit_exact(gi, dtype):
     idx = rand_indices(rng, 2, [22] * 3, 2500)
     res = _tables(idx, 2, [22] * 3, ks, st, pad, dil, subm)
     pf, pb = res[2], res[3]
-    x = torch.randn(idx.shape[0], 16).to(DEV, dtype)
+    x = torch.randn(idx.shape[0], C).to(DEV, dtype)
     n_out = pf.shape[1]
     out, count = pool.avgpool_forward(x, pf, n_out)
     ref, ref_count = orc.avgpool_fwd(x.cpu().numpy(), pf.cpu().numpy())
     np.testing.assert_array_equal(count.cpu().numpy(), ref_count)
     np.testing.assert_array_equal(out.cpu().numpy(), ref)
-    g = torch.randn(n_out, 16).to(DEV, dtype)
+    g = torch.randn(n_out, C).to(DEV, dtype)
     dx = pool.avgpool_backward(g, pb, count)
     ref_dx = orc.avgpool_bwd(g.cpu().numpy(), ref_count, pb.cpu().numpy())
     np.testing.assert_array_equal(dx.cpu().numpy(), ref_dx)
+
+
+def _unaligned(t: torch.Tensor) -> torch.Tensor:
+    """A contiguous copy of ``t`` whose data starts one element past a 16-byte
+    boundary (the pool entry points then take their element-wise kernels)."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    u = buf[1:].view(t.shape)
+    u.copy_(t)
+    assert u.data_ptr() % 16 != 0
+    return u
+
+
+@pytest.mark.parametrize("dtype,C,unaligned", [
+    (torch.float16, 2048, False),  # 256 pieces per row: one row per vector workgroup
+    (torch.float32, 1100, False),  # 275 pieces: element-wise kernels
+    (torch.float16, 24, True),     # whole pieces, unaligned data: element-wise kernels
+])
+def test_pool_wide_and_unaligned_rows(dtype, C, unaligned):
+    from spconv_triton.pytorch._impl import pool
+
+    ks, st, pad, dil, subm = GEOMS[1]
+    rng = np.random.default_rng(77)
+    idx = rand_indices(rng, 2, [22] * 3, 1200)
+    res = _tables(idx, 2, [22] * 3, ks, st, pad, dil, subm)
+    pf, pb = res[2], res[3]
+    n_out = pf.shape[1]
+    x = (torch.round(torch.randn(idx.shape[0], C) * 2) / 2).to(DEV, dtype)
+    g = torch.randn(n_out, C).to(DEV, dtype)
+    if unaligned:
+        x, g = _unaligned(x), _unaligned(g)
+    xn, gn = x.cpu().numpy(), g.cpu().numpy()
+    out = pool.maxpool_forward(x, pf, n_out)
+    ref = orc.maxpool_fwd(xn, pf.cpu().numpy())
+    np.testing.assert_array_equal(out.cpu().numpy(), ref.astype(xn.dtype))
+    outa = _unaligned(out) if unaligned else out
+    dx = pool.maxpool_backward(x, outa, g, pb)
+    ref_dx = orc.maxpool_bwd(xn, out.cpu().numpy(), gn, pb.cpu().numpy())
+    np.testing.assert_array_equal(dx.cpu().numpy(), ref_dx.astype(xn.dtype))
+    avg, count = pool.avgpool_forward(x, pf, n_out)
+    ref_avg, ref_count = orc.avgpool_fwd(xn, pf.cpu().numpy())
+    np.testing.assert_array_equal(count.cpu().numpy(), ref_count)
+    np.testing.assert_array_equal(avg.cpu().numpy(), ref_avg)
+    dxa = pool.avgpool_backward(g, pb, count)
+    ref_dxa = orc.avgpool_bwd(gn, ref_count, pb.cpu().numpy())
+    np.testing.assert_array_equal(dxa.cpu().numpy(), ref_dxa)
