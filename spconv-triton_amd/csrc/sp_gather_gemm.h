@@ -137,6 +137,32 @@ __device__ __forceinline__ bool block_tile(int64_t M, int N, int64_t* tile, int*
   return *tile < nt;
 }
 
+// Tile and first output column of a staged-kernel workgroup.  One column
+// block (N <= 64): as block_tile.  Several: a 1-D grid of
+// 8 * gy * ceil(ntiles / 8) workgroups in which tile t runs on XCD t % 8 and
+// its gy column blocks are back to back in that XCD's queue, so they stage
+// the same rows through its L2 at about the same time, while consecutive
+// tiles are spread over the XCDs (in mask order the tiles' costs vary along
+// the table, so contiguous ranges per XCD leave some XCDs far more work).
+// Measured, fp16 forward: LiDAR 50k 256 -> 256 in mask order 183 -> 149 us,
+// 1024^3 surface 256 -> 256 in mask order 675 -> 572 us, LiDAR natural
+// 168 -> 153 us (the 2-D grid, whose column blocks of a tile land on
+// different XCDs, against this one).  Returns false for the padding
+// workgroups past the last tile, which must exit at once.
+__device__ __forceinline__ bool staged_tile(int64_t M, int N, int64_t* tile, int* n0) {
+  const int gy = (N + 63) / 64;
+  if (gy == 1) {
+    *tile = xcd_tile(blockIdx.x, gridDim.x);
+    *n0 = 0;
+    return true;
+  }
+  const int64_t nt = (M + kTileRows - 1) / kTileRows;
+  const int64_t b = blockIdx.x, x = b % 8, k = b / 8;
+  *tile = (k / gy) * 8 + x;
+  *n0 = int(k % gy) * 64;
+  return *tile < nt;
+}
+
 // LDS writes of this wave are complete, then the workgroup barrier.  Written
 // as one asm statement with a memory clobber: the compiler neither moves LDS
 // accesses across it nor adds waits for outstanding global loads (which the
@@ -511,9 +537,10 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int h = lane >> 5, l32 = lane & 31;
-  const int64_t tile = xcd_tile(blockIdx.x, gridDim.x);
+  int64_t tile;
+  int n0;
+  if (!staged_tile(M, N, &tile, &n0)) return;
   const int64_t slot0 = tile * kTileRows + wave * 64;
-  const int n0 = blockIdx.y * 64;
 
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, nb.a_bytes);
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bt, nb.bt_bytes);

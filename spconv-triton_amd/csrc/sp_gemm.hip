@@ -569,12 +569,12 @@ static int launch_staged(dim3 grid, hipStream_t s, const T* A, const T* bt, cons
 template <typename T, typename OutT, bool VEC>
 static int launch_modes(unsigned gx, unsigned gy, hipStream_t s, const T* A, const T* bt,
                         const int32_t* pairs, OutT* o, GemmBufs nb, const GemmCall& c) {
-  if (!c.planned) {  // grid order: block_tile
-    const uint64_t nwg = gy == 1 ? uint64_t(gx) : 8ull * gy * ((uint64_t(gx) + 7) / 8);
-    SP_CHECK_ARG(nwg <= uint64_t(kMaxGridX), "gemm: too many tiles");
+  // grid order: block_tile (direct) or staged_tile (staged), both 1-D
+  const uint64_t nwg = gy == 1 ? uint64_t(gx) : 8ull * gy * ((uint64_t(gx) + 7) / 8);
+  SP_CHECK_ARG(nwg <= uint64_t(kMaxGridX), "gemm: too many tiles");
+  if (!c.planned)
     return launch_direct<T, OutT, VEC>(dim3{unsigned(nwg), 1u, 1u}, s, A, bt, pairs, o, nb, c);
-  }
-  return launch_staged<T, OutT, VEC>(dim3{gx, gy, 1u}, s, A, bt, pairs, o, nb, c);
+  return launch_staged<T, OutT, VEC>(dim3{unsigned(nwg), 1u, 1u}, s, A, bt, pairs, o, nb, c);
 }
 
 // The mask tables (pair_mask / mask_argsort) of the reference's masked path

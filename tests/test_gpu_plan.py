@@ -331,9 +331,9 @@ def test_auto_row_order_decision():
     # (voxels, grid, reordered): 30000 in 100^3 has 1.7 pairs per row, yet
     # nearly every offset has a pair in each natural tile (6.5 % of the MFMA
     # work is on pairs) and the mask order cuts the work to 23 %; in 40^3 the
-    # mask order only cuts it to 67 %; 20^3 is dense (67 % on pairs); in
-    # 200^3 rows are isolated, so natural tiles already hold only the centre
-    # offset (30 % on pairs)
+    # mask order only cuts it to 66 %; 20^3 is dense (67 % on pairs); in
+    # 200^3 rows are isolated and the table has 12 tiles: 37 % of the natural
+    # work is on pairs, and the mask order would cut it only to 94 %
     for n, grid, sparse in ((30000, 100, True), (6000, 40, False), (6000, 20, False),
                             (3000, 200, False)):
         idx = rand_indices(rng, 1, [grid] * 3, n)
