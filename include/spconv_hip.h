@@ -123,11 +123,15 @@ int sp_pairgen_subm_grid(const sp_geom* g, const int32_t* indices, int64_t n, in
 /* Regular / transposed convolution, phase 1: deduplicate the candidate output
  * keys, sort them ascending (batch-major linear key), and rank them.  Blocks
  * until the count is known and stores it in *n_out (0 = every point vanished).
+ * *n_pairs (nullable) receives the number of candidates, i.e. the valid
+ * entries of the gather table (before any n_keep truncation in phase 2),
+ * read back in the same synchronisation.
  * Replaces K1 + out_lin[valid] + torch.unique + K3 of
  *   spconv_triton/pytorch/_impl/pairs.py:126-220 (regular/transpose branch)
  *   spconv_triton/pytorch/_impl/pair_kernels.py:37-94, :298-392 */
 int sp_pairgen_conv_build(const sp_geom* g, const int32_t* indices, int64_t n,
-                          void* ws, size_t ws_bytes, int64_t* n_out, void* stream);
+                          void* ws, size_t ws_bytes, int64_t* n_out, int64_t* n_pairs,
+                          void* stream);
 
 /* Phase 2: output coordinates and gather tables for the first n_keep outputs
  * (n_keep <= n_out; smaller values implement num_out_act_bound,
@@ -241,11 +245,14 @@ int sp_conv_gemm_ordered(const void* a, int32_t dtype, int64_t n_src, const void
                          void* stream);
 
 /* out[k, i] = pairs[k, order[i]] for a gather table pairs [kv, M] (-1 where
- * order[i] is outside 0..M-1).  Builds the pairs_perm of sp_conv_gemm_ordered
+ * order[i] is outside 0..M-1).  order_words (nullable, kv <= 32): the mask
+ * word of row order[i] at [i] (bit k set iff pairs[k, order[i]] >= 0, e.g. the
+ * sorted pair_mask of sp_mask_sort); entries of clear bits are then written
+ * as -1 without being read.  Builds the pairs_perm of sp_conv_gemm_ordered
  * (the reference indexes the table through mask_argsort inside its kernel,
  * gemm.py:501-568). */
 int sp_permute_table(const int32_t* pairs, int64_t kv, int64_t M, const int32_t* order,
-                     int32_t* out, void* stream);
+                     const uint32_t* order_words, int32_t* out, void* stream);
 
 /* Work statistics of a gather table [kv, M] (kv <= 512) in its own row order, added into
  * stats[0..2] (int64, zeroed by the caller): the pairs (entries in

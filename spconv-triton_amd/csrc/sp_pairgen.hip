@@ -558,12 +558,20 @@ static void conv_layout(W& w, const GeomDev& g, int64_t n, bool key64, ConvWs* o
 // that prefix plus the popcount of its word's lower bits, i.e. its rank in
 // ascending key order (torch.unique's order, as the hash path's sort gives).
 // The set bits, read in word order, are the sorted unique keys themselves.
+// The bitmap's passes cost in proportion to the output volume, the hash
+// path's in proportion to the candidates (n * kv, each an insert with probing,
+// then a radix sort and a ranking pass): the bitmap is taken up to 4096 cells
+// per input row or 1024 per candidate.  (Measured on a transposed k3 s2 conv
+// of 50k uniform voxels in 41 x 1600 x 1408: 749M output cells, 15k per row
+// but 555 per candidate; the hash path's insert alone took 270 us.)
 constexpr int64_t kBitmapCellsPerRow = 4096;
+constexpr int64_t kBitmapCellsPerCandidate = 1024;
 
 static bool conv_bitmap(const GeomDev& g, int64_t n, bool key64) {
   if (key64) return false;
   const double vol = double(g.batch) * double(prod_shape(g.out_shape, g.ndim));
-  return vol <= double(kBitmapCellsPerRow) * double(n);
+  return vol <= double(kBitmapCellsPerRow) * double(n) ||
+         vol <= double(kBitmapCellsPerCandidate) * double(n) * double(g.kv);
 }
 
 struct BitmapWs {
@@ -584,30 +592,42 @@ static void bitmap_layout(W& w, const GeomDev& g, BitmapWs* out) {
   if (out) *out = BitmapWs{bits, prefix, total, sws, words};
 }
 
+// Adds every lane's count to *total with one atomic per wave.
+__device__ __forceinline__ void wave_count(uint32_t cnt, unsigned long long* total) {
+  for (int off = 32; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+  if (lane_id() == 0 && cnt != 0) atomicAdd(total, (unsigned long long)cnt);
+}
+
 // One thread per input row j: set the bits of its candidate outputs.  The kv
 // candidates of a row come in key order along the fastest dimension, so runs
 // in one word are ORed together before the atomic.
+// The candidates (the table's pairs) are counted into *npairs.
 __global__ __launch_bounds__(256) void conv_mark(const int32_t* __restrict__ idx, int64_t n,
-                                                 GeomDev g, uint32_t* __restrict__ bits) {
+                                                 GeomDev g, uint32_t* __restrict__ bits,
+                                                 unsigned long long* __restrict__ npairs) {
   const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (j >= n) return;
-  const Coord c = load_coord(idx, j, g);
-  int off[4] = {0, 0, 0, 0};
-  uint32_t cw = 0, cb = 0;  // pending word and its bits (cb == 0: none)
-  for (int k = 0; k < g.kv; ++k) {
-    uint64_t key;
-    if (candidate_key<int32_t>(g, c, off, &key)) {
-      const uint32_t w = uint32_t(key >> 5), b = 1u << uint32_t(key & 31u);
-      if (cb != 0 && w != cw) {
-        atomicOr(&bits[cw], cb);
-        cb = 0;
+  uint32_t cnt = 0;
+  if (j < n) {
+    const Coord c = load_coord(idx, j, g);
+    int off[4] = {0, 0, 0, 0};
+    uint32_t cw = 0, cb = 0;  // pending word and its bits (cb == 0: none)
+    for (int k = 0; k < g.kv; ++k) {
+      uint64_t key;
+      if (candidate_key<int32_t>(g, c, off, &key)) {
+        const uint32_t w = uint32_t(key >> 5), b = 1u << uint32_t(key & 31u);
+        if (cb != 0 && w != cw) {
+          atomicOr(&bits[cw], cb);
+          cb = 0;
+        }
+        cw = w;
+        cb |= b;
+        ++cnt;
       }
-      cw = w;
-      cb |= b;
+      odometer_next(g, off);
     }
-    odometer_next(g, off);
+    if (cb != 0) atomicOr(&bits[cw], cb);
   }
-  if (cb != 0) atomicOr(&bits[cw], cb);
+  wave_count(cnt, npairs);
 }
 
 __global__ __launch_bounds__(256) void popc_words(const uint32_t* __restrict__ bits, int64_t words,
@@ -701,20 +721,27 @@ static void subm_layout(W& w, int64_t n, bool key64, void** ta, int32_t** tv, in
   *cap_out = cap;
 }
 
+// counter[0]: unique keys; the candidates (the table's pairs) are counted
+// into *npairs.
 template <class Table, typename KeyT>
 __global__ __launch_bounds__(256) void conv_insert(const int32_t* __restrict__ idx, int64_t n,
                                                    GeomDev g, Table t, KeyT* __restrict__ list,
-                                                   uint32_t* __restrict__ counter, int64_t bound) {
+                                                   uint32_t* __restrict__ counter, int64_t bound,
+                                                   unsigned long long* __restrict__ npairs) {
   const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const bool live = j < n;
   Coord c;
   if (live) c = load_coord(idx, j, g);
   else c.ok = false;
   int off[4] = {0, 0, 0, 0};
+  uint32_t cnt = 0;
   for (int k = 0; k < g.kv; ++k) {
     uint64_t key = 0;
     bool fresh = false;
-    if (live && candidate_key<KeyInt<Table>>(g, c, off, &key)) fresh = t.insert(key, 0);
+    if (live && candidate_key<KeyInt<Table>>(g, c, off, &key)) {
+      fresh = t.insert(key, 0);
+      ++cnt;
+    }
     // wave-aggregated append of newly inserted keys
     const uint64_t b = __ballot(fresh);
     if (b) {
@@ -729,6 +756,7 @@ __global__ __launch_bounds__(256) void conv_insert(const int32_t* __restrict__ i
     }
     odometer_next(g, off);
   }
+  wave_count(cnt, npairs);
 }
 
 template <class Table, typename KeyT>
@@ -1016,7 +1044,7 @@ int sp_pairgen_subm_grid(const sp_geom* g, const int32_t* indices, int64_t n, in
 }
 
 int sp_pairgen_conv_build(const sp_geom* g, const int32_t* indices, int64_t n, void* ws,
-                          size_t ws_bytes, int64_t* n_out, void* stream) {
+                          size_t ws_bytes, int64_t* n_out, int64_t* n_pairs, void* stream) {
   GeomDev d;
   int rc = make_geom(g, &d);
   if (rc) return rc;
@@ -1036,7 +1064,10 @@ int sp_pairgen_conv_build(const sp_geom* g, const int32_t* indices, int64_t n, v
     fill_i32x4<<<unsigned(fb < 4096 ? fb : 4096), 256, 0, s>>>(
         reinterpret_cast<int32_t*>(b.bits), b.words, 0);
     SP_LAUNCHED();
-    conv_mark<<<unsigned(cdiv(n, 256)), 256, 0, s>>>(indices, n, d, b.bits);
+    // total[0]: set bits (from the scan); total[32..33]: the pair count
+    auto* npairs = reinterpret_cast<unsigned long long*>(b.total + 32);
+    SP_HIP(hipMemsetAsync(npairs, 0, sizeof(unsigned long long), s));
+    conv_mark<<<unsigned(cdiv(n, 256)), 256, 0, s>>>(indices, n, d, b.bits, npairs);
     SP_LAUNCHED();
     const int64_t pbk = cdiv(b.words, 256);
     SP_CHECK_ARG(pbk <= kMaxGridX, "pairgen: output volume too large");
@@ -1044,16 +1075,18 @@ int sp_pairgen_conv_build(const sp_geom* g, const int32_t* indices, int64_t n, v
     SP_LAUNCHED();
     rc = exclusive_scan_u32(b.prefix, b.prefix, b.words, b.total, b.scan_ws, s);
     if (rc) return rc;
-    uint32_t h = 0;
-    SP_HIP(hipMemcpyAsync(&h, b.total, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+    uint32_t h[34] = {};
+    SP_HIP(hipMemcpyAsync(h, b.total, sizeof(h), hipMemcpyDeviceToHost, s));
     SP_HIP(hipStreamSynchronize(s));
-    *n_out = int64_t(h);
+    *n_out = int64_t(h[0]);
+    if (n_pairs) *n_pairs = int64_t(uint64_t(h[32]) | (uint64_t(h[33]) << 32));
     return SP_OK;
   }
   ConvWs w;
   conv_layout(c, d, n, key64, &w);
   SP_HIP(hipMemsetAsync(w.flags, 0, 256, s));
   SP_HIP(hipMemsetAsync(w.counter, 0, 256, s));
+  auto* npairs = reinterpret_cast<unsigned long long*>(w.counter + 32);
   rc = launch_fill_u64(static_cast<uint64_t*>(w.table_a), int64_t(w.cap), kEmpty64, s);
   if (rc) return rc;
   const unsigned blocks = unsigned(cdiv(n, 256));
@@ -1062,18 +1095,20 @@ int sp_pairgen_conv_build(const sp_geom* g, const int32_t* indices, int64_t n, v
     if (rc) return rc;
     Table64 t{static_cast<uint64_t*>(w.table_a), w.table_vals, w.cap - 1, w.flags};
     conv_insert<Table64, uint64_t><<<blocks, 256, 0, s>>>(
-        indices, n, d, t, static_cast<uint64_t*>(w.list), w.counter, w.bound);
+        indices, n, d, t, static_cast<uint64_t*>(w.list), w.counter, w.bound, npairs);
   } else {
     Table32 t{static_cast<uint64_t*>(w.table_a), w.cap - 1, w.flags};
     conv_insert<Table32, uint32_t><<<blocks, 256, 0, s>>>(
-        indices, n, d, t, static_cast<uint32_t*>(w.list), w.counter, w.bound);
+        indices, n, d, t, static_cast<uint32_t*>(w.list), w.counter, w.bound, npairs);
   }
   SP_LAUNCHED();
-  uint32_t host[2] = {0, 0};
-  SP_HIP(hipMemcpyAsync(&host[0], w.counter, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
-  SP_HIP(hipMemcpyAsync(&host[1], w.flags, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  uint32_t host[34] = {};  // counter[0]: unique keys, [32..33]: pairs
+  uint32_t overflow = 0;
+  SP_HIP(hipMemcpyAsync(host, w.counter, sizeof(host), hipMemcpyDeviceToHost, s));
+  SP_HIP(hipMemcpyAsync(&overflow, w.flags, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
   SP_HIP(hipStreamSynchronize(s));
-  if (host[1]) return set_error(SP_ERR_HASH_FULL, "pairgen: coordinate hash overflow");
+  if (overflow) return set_error(SP_ERR_HASH_FULL, "pairgen: coordinate hash overflow");
+  if (n_pairs) *n_pairs = int64_t(uint64_t(host[32]) | (uint64_t(host[33]) << 32));
   const int64_t cnt = int64_t(host[0]);
   if (cnt > w.bound) return set_error(SP_ERR_HASH_FULL, "pairgen: %lld keys > bound %lld",
                                       (long long)cnt, (long long)w.bound);

@@ -335,15 +335,24 @@ __global__ __launch_bounds__(256) void table_stats_kernel(const int32_t* __restr
 
 // out[k, i] = pairs[k, order[i]]: the table in a given row order (-1 where
 // order[i] is not a row).
+// With the rows' mask words (kv <= 32), entries whose bit is clear are -1
+// without a read: the reads are random (one cache line per entry), and a
+// table with few pairs per row has mostly clear bits.
 __global__ __launch_bounds__(256) void permute_table_kernel(const int32_t* __restrict__ pairs,
                                                             int64_t M, int kv,
                                                             const int32_t* __restrict__ order,
+                                                            const uint32_t* __restrict__ words,
                                                             int32_t* __restrict__ out) {
   const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (i >= M) return;
   const int32_t src = order[i];
   const bool ok = src >= 0 && src < M;
-  for (int k = 0; k < kv; ++k) out[int64_t(k) * M + i] = ok ? pairs[int64_t(k) * M + src] : -1;
+  const uint32_t w = words ? words[i] : 0xFFFFFFFFu;
+  for (int k = 0; k < kv; ++k) {
+    int32_t v = -1;
+    if (ok && ((w >> (k & 31)) & 1u)) v = pairs[int64_t(k) * M + src];
+    out[int64_t(k) * M + i] = v;
+  }
 }
 
 template <int NP>
@@ -421,14 +430,16 @@ int sp_table_stats(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_src, i
 }
 
 int sp_permute_table(const int32_t* pairs, int64_t kv, int64_t M, const int32_t* order,
-                     int32_t* out, void* stream) {
+                     const uint32_t* order_words, int32_t* out, void* stream) {
   SP_CHECK_ARG(kv >= 1 && M >= 0, "permute table: bad sizes");
   if (M == 0) return SP_OK;
   SP_CHECK_ARG(pairs && order && out, "permute table: null pointer");
+  SP_CHECK_ARG(!order_words || kv <= 32, "permute table: mask words need kv <= 32, not %lld",
+               (long long)kv);
   const int64_t nb = cdiv(M, int64_t(256));
   SP_CHECK_ARG(nb <= kMaxGridX && kv < 65536, "permute table: too many rows");
   permute_table_kernel<<<unsigned(nb), 256, 0, as_stream(stream)>>>(pairs, M, int(kv), order,
-                                                                     out);
+                                                                     order_words, out);
   SP_LAUNCHED();
   return SP_OK;
 }

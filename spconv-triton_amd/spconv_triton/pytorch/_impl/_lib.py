@@ -95,7 +95,8 @@ _SIGNATURES = {
     "sp_pairgen_subm_grid_cells": (_I64, [_GP, _I64]),
     "sp_pairgen_subm_grid": (ctypes.c_int, [_GP, _P, _I64, _P, _P, _P, _P, _P, _I64,
                                             ctypes.c_uint32, _P]),
-    "sp_pairgen_conv_build": (ctypes.c_int, [_GP, _P, _I64, _P, _SZ, ctypes.POINTER(_I64), _P]),
+    "sp_pairgen_conv_build": (ctypes.c_int, [_GP, _P, _I64, _P, _SZ, ctypes.POINTER(_I64),
+                                             ctypes.POINTER(_I64), _P]),
     "sp_pairgen_conv_fill": (ctypes.c_int, [_GP, _P, _I64, _P, _SZ, _I64, _P, _P, _P, _P, _P]),
     "sp_mask_words": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),
     "sp_mask_sort_workspace_size": (_SZ, [_I64, _I32]),
@@ -115,7 +116,7 @@ _SIGNATURES = {
                                             _I64, _P, _SZ, _P, _I32, _P]),
     "sp_conv_gemm_ordered": (ctypes.c_int, [_P, _I32, _I64, _P, _I64, _I64, _I64, _I32, _I32, _P,
                                             _I64, _P, _P, _SZ, _P, _I32, _P]),
-    "sp_permute_table": (ctypes.c_int, [_P, _I64, _I64, _P, _P, _P]),
+    "sp_permute_table": (ctypes.c_int, [_P, _I64, _I64, _P, _P, _P, _P]),
     "sp_table_stats": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P]),
     "sp_conv_fwd": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _P, _I64, _P,
                                    _P, _P, _P, _I32, _P, _SZ, _P]),

@@ -190,6 +190,25 @@ ROW_ORDER = os.environ.get("SPCONV_GEMM_ROW_ORDER", "auto")
 ORDER_MIN_WORK = 128 * 128
 ORDER_MAX_EFFICIENCY = 0.35
 ORDER_MAX_WORK_RATIO = 0.35
+#: A strided or transposed convolution's rulebook is often used once (rebuilt
+#: every pass), so waiting for a second use would never reorder it.  Its pair
+#: generation counts the table's pairs in passing; a table with at most
+#: FIRST_USE_MAX_PAIRS_PER_ROW pairs per row (a transposed convolution of
+#: sparse voxels has one pair per output, while a natural tile of its sorted
+#: outputs holds nearly every offset) whose natural GEMM would multiply at
+#: least FIRST_USE_MIN_MACS (rows * kv * C * K) is decided at its first wide
+#: call instead: the mask sort, the permuted table, its plan and the two
+#: statistics read-backs cost ~0.1-0.3 ms, which a smaller GEMM does not
+#: repay (measured: the ResUNet step's 151k-row 256 -> 128 k2 s2 inverse
+#: convolution, 4e10 MACs, made the step 0.4 ms slower; the transposed k3 s2
+#: 256 -> 256 convolution of 50k voxels, 2.4e12 MACs, went 3.1 -> 2.2 ms).
+FIRST_USE_MAX_PAIRS_PER_ROW = 1.5
+FIRST_USE_MIN_MACS = 2e11
+#: With at most SURE_PAIRS_PER_ROW pairs per row the mask order's tiles hold
+#: about one offset each, so the statistics are not read back (two
+#: synchronisations): the strided k3 s2 256 -> 256 convolution of 50k uniform
+#: voxels (1.007 pairs per output) 0.56 -> 0.45 ms.
+SURE_PAIRS_PER_ROW = 1.05
 _PLAN_MAX_KV = 64  # kv range of the gather plans (sp_gather_plan_bytes)
 _STATS_MAX_KV = 512  # kv range of sp_table_stats
 
@@ -209,23 +228,37 @@ def table_stats(pairs: torch.Tensor, n_src: int) -> tuple[int, int, int]:
     return tuple(int(v) for v in _launch_table_stats(pairs, n_src).cpu())
 
 
-def mask_order(pairs: torch.Tensor) -> torch.Tensor:
+def mask_order(pairs: torch.Tensor, with_words: bool = False):
     """Stable argsort of the rows' masks of a [kv, M] table, as the reference's
-    mask_argsort (pairs.py:356-392) orders them: int32 [M]."""
+    mask_argsort (pairs.py:356-392) orders them: int32 [M].  with_words: also
+    the sorted mask words ([M, ceil(kv/32)], row order[i] at i)."""
     from . import pairs as _pairs
     kv = pairs.shape[0]
     words = _pairs.mask_words(pairs)
-    _, ar = _pairs.sort_mask_words(words, kv, _pairs.split_masks(kv, False), True)
-    return ar[0]
+    pm, ar = _pairs.sort_mask_words(words, kv, _pairs.split_masks(kv, False), True)
+    return (ar[0], pm[0]) if with_words else ar[0]
 
 
-def permute_table(pairs: torch.Tensor, order: torch.Tensor) -> torch.Tensor:
-    """out[k, i] = pairs[k, order[i]] (``sp_permute_table``)."""
+def permute_table(pairs: torch.Tensor, order: torch.Tensor,
+                  order_words: torch.Tensor | None = None) -> torch.Tensor:
+    """out[k, i] = pairs[k, order[i]] (``sp_permute_table``); order_words: the
+    mask words of the rows in that order (kv <= 32), which lets the kernel
+    skip the reads of empty entries."""
     kv, M = pairs.shape
     out = torch.empty_like(pairs)
-    _lib.check(_lib.lib().sp_permute_table(_lib.ptr(pairs), kv, M, _lib.ptr(order), _lib.ptr(out),
+    _lib.check(_lib.lib().sp_permute_table(_lib.ptr(pairs), kv, M, _lib.ptr(order),
+                                           _lib.ptr(order_words), _lib.ptr(out),
                                            _lib.stream_of(pairs.device)), "sp_permute_table")
     return out
+
+
+def _decide_at_first_use(pairs: torch.Tensor, work: int) -> bool:
+    """A table whose pair count (from its pair generation) shows few pairs per
+    row, under a large GEMM: see FIRST_USE_MAX_PAIRS_PER_ROW."""
+    npairs = getattr(pairs, "_spconv_triton_npairs", None)
+    kv, M = pairs.shape
+    return (npairs is not None and kv >= 8 and npairs <= FIRST_USE_MAX_PAIRS_PER_ROW * M
+            and float(M) * kv * work >= FIRST_USE_MIN_MACS)
 
 
 def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool = True):
@@ -234,7 +267,8 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool 
     ROW_ORDER), else None.  ``plan_ok``: the call may use a gather plan.
 
     In auto mode only tables that wide layers use more than once are looked
-    at: the first wide call on a table runs in natural order and launches
+    at (or, see FIRST_USE_MAX_PAIRS_PER_ROW, tables with few pairs per row):
+    the first wide call on a table runs in natural order and launches
     nothing (a table rebuilt every step costs nothing); the second reads the
     table's statistics back (a stream synchronization) and, when they pass,
     sorts the masks, permutes the table and reads the permuted table's
@@ -269,7 +303,7 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool 
         return None  # narrow layers never start the decision
     if torch.cuda.is_current_stream_capturing():
         return None  # a graph being captured must not synchronize: decide on a later call
-    if mode == "auto" and step == "start":
+    if mode == "auto" and step == "start" and not _decide_at_first_use(pairs, work):
         pairs._spconv_triton_order = (stamp, "seen")
         return None
 
@@ -279,12 +313,14 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool 
         return 256 * stats[1] if planned else 64 * stats[2]
 
     variant = None
-    natural = table_stats(pairs, n_src) if mode == "auto" else None
+    npairs = getattr(pairs, "_spconv_triton_npairs", None)
+    sure = mode == "mask" or (npairs is not None and npairs <= SURE_PAIRS_PER_ROW * M)
+    natural = table_stats(pairs, n_src) if not sure else None
     done = mfma_rows(natural) if natural is not None else 0
-    if mode == "mask" or (done > 0 and natural[0] < ORDER_MAX_EFFICIENCY * done):
-        order = mask_order(pairs)
-        perm = permute_table(pairs, order)
-        if mode == "mask" or mfma_rows(table_stats(perm, n_src)) <= ORDER_MAX_WORK_RATIO * done:
+    if sure or (done > 0 and natural[0] < ORDER_MAX_EFFICIENCY * done):
+        order, words = mask_order(pairs, with_words=True)
+        perm = permute_table(pairs, order, words if kv <= 32 else None)
+        if sure or mfma_rows(table_stats(perm, n_src)) <= ORDER_MAX_WORK_RATIO * done:
             plan = gather_plan(perm, n_src) if planned else None
             variant = (order, perm, plan)
     pairs._spconv_triton_order = (stamp, variant if variant is not None else "natural")

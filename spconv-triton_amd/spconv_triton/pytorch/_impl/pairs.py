@@ -197,8 +197,9 @@ def _generate(indices, batch_size, spatial_shape, ksize, stride, padding, dilati
         return _Tables(indices, pf, pb, words, None, N, npl)
     ws = _lib.workspace(L.sp_pairgen_workspace_size(g, N), device)
     n_out = ctypes.c_int64(0)
+    n_pairs = ctypes.c_int64(0)
     _lib.check(L.sp_pairgen_conv_build(g, _lib.ptr(idx), N, _lib.ptr(ws), ws.numel(), n_out,
-                                       stream), "sp_pairgen_conv_build")
+                                       n_pairs, stream), "sp_pairgen_conv_build")
     n_out = int(n_out.value)
     if n_out == 0:
         raise ValueError(_POINT_VANISH_MSG.format(spatial_shape, ksize, stride, padding, dilation))
@@ -216,6 +217,12 @@ def _generate(indices, batch_size, spatial_shape, ksize, stride, padding, dilati
     words_fwd = None
     if want_words_fwd:
         words_fwd = mask_words(pf)
+    for table in (pf, pb):
+        if table is not None:
+            # the tables' valid entries, known without a further
+            # synchronisation: the GEMM's row-order decision reads them
+            # (gemm.row_order_variant)
+            table._spconv_triton_npairs = int(n_pairs.value)
     _attach_coords(pf, out_inds, out_shape, batch_size)
     _attach_coords(pb, idx, spatial_shape, batch_size)
     return _Tables(out_inds, pf, pb, words_fwd, words_bwd, n_out)

@@ -119,8 +119,9 @@ def _align256(v):
 
 def _conv_uses_bitmap(batch, g, n):
     """Whether sp_pairgen_conv_build takes its occupancy-bitmap path (int32
-    keys, at most 4096 output cells per input row): its workspace is then
-    the bitmap, the word prefix, a counter and the scan's chunk sums."""
+    keys, at most 4096 output cells per input row or 1024 per candidate): its
+    workspace is then the bitmap, the word prefix, a counter and the scan's
+    chunk sums."""
     from spconv_triton.pytorch._impl import _lib, pairs as P
 
     shape, ks, st, pad, dil, op, subm, tr = g
@@ -151,7 +152,8 @@ def test_conv_bitmap_and_hash_paths_bit_exact(gi):
                                               dil, op, False, tr)))
 
     scale = 8
-    while 3 * out_volume(scale) <= 4096 * 3 * n:
+    kv = int(np.prod(ks))
+    while 3 * out_volume(scale) <= max(4096, 1024 * kv) * 3 * n:
         scale *= 2
     for s_ in (1, scale):
         big = [x * s_ for x in shape]
@@ -161,6 +163,11 @@ def test_conv_bitmap_and_hash_paths_bit_exact(gi):
         for is_train in (True, False):
             res, exp, t = _igemm(idx, 3, g, is_train)
             _compare_igemm(res, exp, t, False, is_train)
+            # the pair count both paths return with the output count
+            n_pairs = int((np.asarray(exp[2]) >= 0).sum())
+            assert res[2]._spconv_triton_npairs == n_pairs
+            if is_train:
+                assert res[3]._spconv_triton_npairs == n_pairs
 
 
 @pytest.mark.parametrize("gi", SUBM_GEOMS)

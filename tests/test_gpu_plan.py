@@ -252,6 +252,13 @@ def test_table_stats_and_permute():
         order_np = rng.permutation(M).astype(np.int32)
         perm = gemm.permute_table(t, torch.from_numpy(order_np).to(DEV))
         np.testing.assert_array_equal(perm.cpu().numpy(), tn[:, order_np])
+        if kv <= 32:
+            # with the rows' mask words the empty entries are not read
+            bits = ((tn[:, order_np] >= 0).astype(np.uint64)
+                    << np.arange(kv, dtype=np.uint64)[:, None]).sum(0).astype(np.uint32)
+            words = torch.from_numpy(bits.view(np.int32).reshape(M, 1)).to(DEV)
+            perm_w = gemm.permute_table(t, torch.from_numpy(order_np).to(DEV), words)
+            np.testing.assert_array_equal(perm_w.cpu().numpy(), tn[:, order_np])
 
 
 def _orders(a, w, bias, transpose, pairs, M):
@@ -348,6 +355,49 @@ def test_auto_row_order_decision():
             assert gemm.row_order_variant(pf, n, 64 * 64) is variant, "decision is memoised"
         else:
             assert pf._spconv_triton_order[1] == "natural"
+
+
+def test_row_order_decided_at_first_use_for_one_pair_per_row():
+    """A transposed convolution of sparse voxels has about one pair per output
+    row, and its rulebook is usually used once: the row order is decided at
+    its first wide call from the pair count its generation returned (no
+    "seen" step), the mask order is taken, and the forward equals the
+    natural-order one bit for bit.  A narrow layer decides nothing."""
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+    from spconv_triton.pytorch._impl import gemm
+
+    rng = np.random.default_rng(21)
+    n, grid = 30000, 300
+    t = torch.from_numpy(rand_indices(rng, 1, [grid] * 3, n)).to(DEV)
+
+    def table():
+        return ops.get_indice_pairs_implicit_gemm(t, 1, [grid] * 3, ConvAlgo.MaskImplicitGemm,
+                                                  [3] * 3, [2] * 3, [0] * 3, [1] * 3, [0] * 3,
+                                                  False, True, is_train=False)[2]
+
+    pf = table()
+    kv, M = pf.shape
+    P = int((pf >= 0).sum())
+    assert pf._spconv_triton_npairs == P
+    C = K = 256
+    assert P <= gemm.FIRST_USE_MAX_PAIRS_PER_ROW * M and M * kv * C * K >= gemm.FIRST_USE_MIN_MACS
+    torch.manual_seed(3)
+    x = torch.randn(n, C, device=DEV).half()
+    w = (torch.randn(K, kv, C, device=DEV) / np.sqrt(kv * C)).half()
+    assert gemm.row_order_variant(pf, n, 64 * 64) is None
+    assert getattr(pf, "_spconv_triton_order", None) is None, "narrow layers decide nothing"
+    out = gemm.conv_forward(x, w, pf, M)
+    assert isinstance(pf._spconv_triton_order[1], tuple), "decided at the first wide call"
+    order = pf._spconv_triton_order[1][0]
+    assert torch.equal(torch.sort(order.long())[0], torch.arange(M, device=DEV))
+    prev = gemm.ROW_ORDER
+    gemm.ROW_ORDER = "natural"
+    try:
+        ref = gemm.conv_forward(x, w, table(), M)
+    finally:
+        gemm.ROW_ORDER = prev
+    assert torch.equal(out, ref)
 
 
 def test_row_order_decision_waits_out_graph_capture():
