@@ -237,12 +237,15 @@ int sp_conv_gemm_planned(const void* a, int32_t dtype, int64_t n_src, const void
  * traversal, which visits rows in mask_argsort order so that a row tile holds
  * rows with similar masks (gemm.py:282-296, the mask_argsort operand of
  * _gather_gemm_kernel :501-568); with the table permuted up front the kernel
- * reads it coalesced. */
+ * reads it coalesced.  thin_tiles != 0 (with a plan): most tiles of
+ * pairs_perm hold at most 4 live offsets (tables of about one pair per row);
+ * a kernel that loads each chunk's rows and weights three chunks ahead runs
+ * them (the others take the direct path inside it).  Results are the same. */
 int sp_conv_gemm_ordered(const void* a, int32_t dtype, int64_t n_src, const void* packed,
                          int64_t K, int64_t kv, int64_t C, int32_t transpose, int32_t has_bias,
                          const int32_t* pairs_perm, int64_t M, const int32_t* row_order,
-                         const void* plan, size_t plan_bytes, void* out, int32_t out_dtype,
-                         void* stream);
+                         const void* plan, size_t plan_bytes, int32_t thin_tiles, void* out,
+                         int32_t out_dtype, void* stream);
 
 /* out[k, i] = pairs[k, order[i]] for a gather table pairs [kv, M] (-1 where
  * order[i] is outside 0..M-1).  order_words (nullable, kv <= 32): the mask

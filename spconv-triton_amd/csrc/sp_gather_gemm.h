@@ -809,3 +809,226 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
   store_tile<OutT>(acc, bias, ro, rows_lds + uint32_t(wave) * 64u * epi_pitch(sizeof(OutT)), slot0,
                    n0, M, N, lane, order);
 }
+
+// ---------------------------------------------------------------------------
+// thin kernel
+// ---------------------------------------------------------------------------
+//
+// Tables with about one pair per row, taken in mask order (a transposed or
+// strided convolution of sparse voxels, a submanifold one of isolated voxels):
+// a tile's rows share one mask, so a tile holds one to four live offsets and
+// each of its chunks only a few MFMA steps.  The staged kernel issues a
+// chunk's rows two steps before it stores them, so there every chunk waits
+// for a memory round trip.  Here the plan's item list (at most kThinItems
+// items, its A address records read once per tile) is the same for every
+// chunk, and a chunk's rows and weight slabs are loaded three chunks ahead
+// into registers: chunk c + 3's loads are issued when chunk c starts and
+// stored to LDS when chunk c + 2 ends, so every wait in the loop is for loads
+// issued two chunks' work earlier.  Items past the tile's own are not multiplied at all.
+// Tiles with more items or more distinct rows than the thin layout holds take
+// the direct path, as overflow tiles do in the staged kernel.  Same
+// summation order as the staged kernel (items ascending inside each chunk,
+// chunks ascending), so results are bit-identical.
+
+constexpr int kThinRows = 320;   // staged rows per tile, including the zero row
+constexpr int kThinItems = 4;    // items a thin tile may hold
+
+struct ThinLds {
+  uint32_t rows_off, slab_off, total;
+};
+
+__host__ __device__ inline ThinLds thin_lds(uint32_t out_size) {
+  ThinLds l;
+  l.rows_off = 0;
+  l.slab_off = l.rows_off + uint32_t(kThinRows * kChunkBytes);
+  l.total = l.slab_off + uint32_t(kThinItems) * kSlabBytes;
+  if (l.total < l.rows_off + epi_bytes(out_size)) l.total = l.rows_off + epi_bytes(out_size);
+  return l;
+}
+
+template <typename T, typename OutT, bool VEC, bool ORDERED>
+__global__ __launch_bounds__(256, 2) void gather_gemm_thin(
+    const T* __restrict__ A, const T* __restrict__ Bt, const int32_t* __restrict__ pairs,
+    const int32_t* __restrict__ order_arg, PlanDev plan, const float* __restrict__ bias,
+    OutT* __restrict__ out, GemmBufs nb, int64_t n_src, int64_t M, int N, int R, int Rp,
+    int kv) {
+  const int32_t* __restrict__ order = ORDERED ? order_arg : nullptr;
+  using frag = typename Mfma<T>::frag;
+  constexpr int V = Mfma<T>::V;
+  constexpr uint32_t ES = sizeof(T);
+  constexpr int kChunk = kChunkBytes / int(ES);  // reduction elements per item
+  constexpr int kPerLane = kThinRows / 64;       // staged rows copied per thread and chunk
+  static_assert(V * ES == 16, "fragments and B slab pieces are 16 bytes");
+  static_assert(kThinRows % 64 == 0 && kThinRows <= kLdsRows, "thin rows");
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int h = lane >> 5, l32 = lane & 31;
+  int64_t tile;
+  int n0;
+  if (!staged_tile(M, N, &tile, &n0)) return;
+  // tiles in reverse order: in mask order the rows with the most bits come
+  // last, and their tiles (the ones the direct path takes, many times longer
+  // than a thin one) should start first rather than set the kernel's end
+  tile = (M + kTileRows - 1) / kTileRows - 1 - tile;
+  const int64_t slot0 = tile * kTileRows + wave * 64;
+
+  const int U = plan.count[tile];
+  const int nact = plan.nact[tile];
+  if (U >= kThinRows || nact > kThinItems) {  // whole workgroup (uniform)
+    direct_tile<T, OutT, VEC>(A, Bt, pairs, bias, out, nb, n_src, M, N, R, Rp, kv, tile, n0, smem,
+                              order);
+    return;
+  }
+
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, nb.a_bytes);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bt, nb.bt_bytes);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(out, nb.out_bytes);
+  const ThinLds L = thin_lds(uint32_t(sizeof(OutT)));
+  unsigned char* rows_lds = smem + L.rows_off;
+  unsigned char* slabs = smem + L.slab_off;
+
+  const uint32_t row_bytes = uint32_t(R) * ES;
+  const uint32_t slab_bytes = uint32_t(N) * V * ES;        // one (offset, r / V) slab of Bt
+  const uint32_t k_bytes = uint32_t(Rp / V) * slab_bytes;  // one offset of Bt
+  const int nrc = Rp / kChunk;                             // chunks per offset
+  const int E = plan.E;
+
+  // ---- per tile: source rows (as A byte offsets), the items' B offsets and
+  // this lane's A address records
+  const int p = tid & 3, ub = tid >> 2;  // this thread copies piece p of rows ub + 64 j
+  uint32_t rowoff[kPerLane];
+  {
+    const int32_t* rows = plan.rows + tile * kLdsRows;
+    int32_t rr[kPerLane];
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) rr[j] = rows[ub + 64 * j];
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) rowoff[j] = rr[j] >= 0 ? uint32_t(rr[j]) * row_bytes : kOob;
+  }
+  uint32_t kb[kThinItems];  // B offset of each item (uniform)
+#pragma unroll
+  for (int i = 0; i < kThinItems; ++i) {
+    const int32_t ko = i < nact ? plan.koff[tile * E + i] : -1;
+    kb[i] = ko >= 0 ? uint32_t(ko) * k_bytes : kBOob;
+  }
+  uint32_t rec[kThinItems];  // A address records: rows l32 and 32 + l32 of this wave
+  {
+    const __amdgpu_buffer_rsrc_t rrec =
+        make_rsrc(plan.addr + tile * E * kTileRows, uint32_t(E) * kTileRows * 2u);
+    const uint32_t rec_lane = uint32_t(wave) * 128u + uint32_t(l32) * 4u;
+#pragma unroll
+    for (int i = 0; i < kThinItems; ++i)
+      rec[i] = __builtin_amdgcn_raw_buffer_load_b32(
+          rrec, i < nact ? uint32_t(i) * 512u + rec_lane : kOob, 0, 0);
+  }
+
+  // ---- loads of one chunk into registers, and their stores into LDS
+  // this thread's piece of every item's B slab: piece gp, column cp
+  const int gp = tid >> 6, cp = n0 + (tid & 63);
+  const uint32_t bpiece = (cp < N ? uint32_t(cp) * V * ES : kColOob) + uint32_t(gp) * slab_bytes;
+  struct Chunk {
+    frag st[kPerLane];
+    uint4 q[kThinItems];
+  };
+  auto load_chunk = [&](int rc, Chunk& ch) {  // past the last chunk: zeros, never stored
+    const int e0 = rc * kChunk + p * V;
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j) {
+      const uint32_t o = rowoff[j];
+      if (VEC)
+        ch.st[j] = buf_frag<T>(ra, (o != kOob && e0 < R && rc < nrc) ? o + uint32_t(e0) * ES : kOob);
+      else
+        ch.st[j] = buf_frag_elems<T>(ra, rc < nrc ? o : kOob, e0, R);
+    }
+    const uint32_t cofs = uint32_t(rc) * 4u * slab_bytes + bpiece;
+#pragma unroll
+    for (int i = 0; i < kThinItems; ++i)
+      ch.q[i] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(rb, rc < nrc ? kb[i] + cofs : kOob, 0, 0));
+  };
+  auto store_chunk = [&](const Chunk& ch) {
+    const uint32_t wbase = chunk_base(uint32_t(ub)) ^ uint32_t(p << 4);
+#pragma unroll
+    for (int j = 0; j < kPerLane; ++j)
+      if (ub + 64 * j <= U)  // rows past the zero row are not stored
+        *reinterpret_cast<frag*>(rows_lds + wbase + 4096u * uint32_t(j)) = ch.st[j];
+#pragma unroll
+    for (int i = 0; i < kThinItems; ++i)
+      if (i < nact)
+        *reinterpret_cast<uint4*>(slabs + uint32_t(i) * kSlabBytes + uint32_t(tid) * 16u) = ch.q[i];
+  };
+
+  // ---- one chunk's MFMAs: the tile's items in ascending order
+  const uint32_t zaddr = chunk_base(uint32_t(U));  // the tile's zero row
+  constexpr bool kSkipDead = sizeof(T) == 4;       // as in the staged kernel
+  floatx16 acc[2][2];
+  zero_acc(acc);
+  auto multiply = [&]() {
+#pragma unroll
+    for (int i = 0; i < kThinItems; ++i) {
+      if (i < nact) {  // uniform
+        const uint32_t t2[2] = {rec[i] & 0xffffu, rec[i] >> 16};
+        bool live[2] = {true, true};
+        if constexpr (kSkipDead) {
+          live[0] = __builtin_amdgcn_ballot_w64(t2[0] != zaddr) != 0;
+          live[1] = __builtin_amdgcn_ballot_w64(t2[1] != zaddr) != 0;
+        }
+        frag a[2][2], b[2][2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+            a[ks][mt] = *reinterpret_cast<const frag*>(rows_lds +
+                                                      (t2[mt] ^ (uint32_t(ks * 2 + h) << 4)));
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt)
+            b[ks][nt] = *reinterpret_cast<const frag*>(slabs + uint32_t(i) * kSlabBytes +
+                                                      uint32_t(ks * 2 + h) * 1024u +
+                                                      uint32_t(nt * 32 + l32) * 16u);
+        }
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+            if (!kSkipDead || live[mt])
+#pragma unroll
+              for (int nt = 0; nt < 2; ++nt) Mfma<T>::mma(a[ks][mt], b[ks][nt], acc[mt][nt]);
+      }
+    }
+  };
+
+  // ---- the chunk loop, unrolled by three so that the register sets are
+  // static: while chunk c is multiplied, chunks c + 1 and c + 2 wait in two
+  // sets (loaded when chunks c - 2 and c - 1 started) and chunk c + 3's loads
+  // fill the third, so a load has three chunks' work to arrive in.  Every
+  // store is unconditional, so no path reaches a load into a set whose
+  // previous loads were not consumed (the compiler would wait for them
+  // first); chunks past the last read zeros and are not multiplied.
+  Chunk c0, c1, c2;
+  load_chunk(0, c0);
+  load_chunk(1, c1);
+  load_chunk(2, c2);
+  store_chunk(c0);
+  __syncthreads();
+  for (int rc = 0; rc < nrc; rc += 3) {
+    load_chunk(rc + 3, c0);
+    multiply();
+    __syncthreads();  // chunk rc's LDS is no longer read
+    store_chunk(c1);
+    __syncthreads();
+    load_chunk(rc + 4, c1);
+    if (rc + 1 < nrc) multiply();
+    __syncthreads();
+    store_chunk(c2);
+    __syncthreads();
+    load_chunk(rc + 5, c2);
+    if (rc + 2 < nrc) multiply();
+    __syncthreads();
+    store_chunk(c0);
+    __syncthreads();
+  }
+  store_tile<OutT>(acc, bias, ro, rows_lds + uint32_t(wave) * 64u * epi_pitch(sizeof(OutT)), slot0,
+                   n0, M, N, lane, order);
+}

@@ -509,6 +509,7 @@ struct GemmCall {
   const float* bias;
   const int32_t* order;  // tile row -> output row, or null (natural order)
   bool vec;
+  bool thin;             // planned: the thin kernel (tiles of at most kThinItems items)
 };
 
 // Raises a kernel's dynamic LDS limit to `bytes` (once per kernel and process).
@@ -564,8 +565,34 @@ static int launch_staged(dim3 grid, hipStream_t s, const T* A, const T* bt, cons
   return SP_OK;
 }
 
-// Planned call: the staged kernel over all tiles (overflow tiles take its
-// direct path).  Unplanned call: the direct kernel over all tiles.
+// LDS of the thin kernel: its own layout, or the direct path's for the tiles
+// it hands over.
+static uint32_t thin_kernel_lds(int kv, uint32_t out_size) {
+  const uint32_t a = thin_lds(out_size).total;
+  const int G = kv < kGroupOffsets ? kv : kGroupOffsets;
+  const uint32_t b = direct_lds(G + kPad, out_size).total;
+  return a > b ? a : b;
+}
+
+template <typename T, typename OutT, bool VEC>
+static int launch_thin(dim3 grid, hipStream_t s, const T* A, const T* bt, const int32_t* pairs,
+                       OutT* o, GemmBufs nb, const GemmCall& c) {
+  const uint32_t lds = thin_kernel_lds(c.kv, uint32_t(sizeof(OutT)));
+  auto kern = c.order ? gather_gemm_thin<T, OutT, VEC, true> : gather_gemm_thin<T, OutT, VEC, false>;
+  static bool attr_set[2] = {false, false};  // per kernel instance
+  int rc = allow_lds(reinterpret_cast<const void*>(kern),
+                     thin_kernel_lds(kPlanMaxKv, uint32_t(sizeof(OutT))),
+                     attr_set[c.order ? 1 : 0]);
+  if (rc) return rc;
+  kern<<<grid, 256, lds, s>>>(A, bt, pairs, c.order, c.plan, c.bias, o, nb, c.n_src, c.M, c.N,
+                              c.R, c.Rp, c.kv);
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
+// Planned call: the staged kernel (or the thin one) over all tiles (overflow
+// tiles take its direct path).  Unplanned call: the direct kernel over all
+// tiles.
 template <typename T, typename OutT, bool VEC>
 static int launch_modes(unsigned gx, unsigned gy, hipStream_t s, const T* A, const T* bt,
                         const int32_t* pairs, OutT* o, GemmBufs nb, const GemmCall& c) {
@@ -574,6 +601,10 @@ static int launch_modes(unsigned gx, unsigned gy, hipStream_t s, const T* A, con
   SP_CHECK_ARG(nwg <= uint64_t(kMaxGridX), "gemm: too many tiles");
   if (!c.planned)
     return launch_direct<T, OutT, VEC>(dim3{unsigned(nwg), 1u, 1u}, s, A, bt, pairs, o, nb, c);
+  if constexpr (VEC) {  // (rows of whole 16-byte pieces; others take the staged kernel)
+    if (c.thin)
+      return launch_thin<T, OutT, VEC>(dim3{unsigned(nwg), 1u, 1u}, s, A, bt, pairs, o, nb, c);
+  }
   return launch_staged<T, OutT, VEC>(dim3{unsigned(nwg), 1u, 1u}, s, A, bt, pairs, o, nb, c);
 }
 
@@ -628,7 +659,7 @@ static int gemm_packed(const void* A, int dtype, int64_t n_src, const void* pack
                        int64_t kv, int64_t C, int transpose, int has_bias, const int32_t* pairs,
                        int64_t M, const int32_t* pm, const int32_t* ar, const void* plan,
                        size_t plan_bytes, void* out, int out_dtype, hipStream_t s,
-                       const int32_t* order = nullptr) {
+                       const int32_t* order = nullptr, bool thin = false) {
   SP_CHECK_ARG(gemm_dtype_ok(dtype), "gemm: feature dtype %d not supported (f16/bf16/f32)", dtype);
   SP_CHECK_ARG(K >= 1 && C >= 1 && kv >= 1 && M >= 0 && n_src >= 0, "gemm: bad sizes");
   SP_CHECK_ARG(K < 65536 && C < 65536 && kv < 65536, "gemm: channel/kernel size too large");
@@ -649,6 +680,7 @@ static int gemm_packed(const void* A, int dtype, int64_t n_src, const void* pack
   c.order = order;
   c.vec = (p.R % vec_of(dtype) == 0) && (reinterpret_cast<uintptr_t>(A) % 16 == 0);
   c.planned = plan != nullptr;
+  c.thin = thin && plan != nullptr;
   c.plan = PlanDev{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0};
   if (plan) {
     SP_CHECK_ARG(kv <= kPlanMaxKv, "gemm: gather plans need kv <= %d", kPlanMaxKv);
@@ -779,12 +811,12 @@ int sp_conv_gemm_planned(const void* a, int32_t dtype, int64_t n_src, const void
 int sp_conv_gemm_ordered(const void* a, int32_t dtype, int64_t n_src, const void* packed,
                          int64_t K, int64_t kv, int64_t C, int32_t transpose, int32_t has_bias,
                          const int32_t* pairs_perm, int64_t M, const int32_t* row_order,
-                         const void* plan, size_t plan_bytes, void* out, int32_t out_dtype,
-                         void* stream) {
+                         const void* plan, size_t plan_bytes, int32_t thin_tiles, void* out,
+                         int32_t out_dtype, void* stream) {
   SP_CHECK_ARG(row_order != nullptr, "gemm: null row order");
   return gemm_packed(a, dtype, n_src, packed, K, kv, C, transpose, has_bias, pairs_perm, M,
                      nullptr, nullptr, plan, plan_bytes, out, out_dtype, as_stream(stream),
-                     row_order);
+                     row_order, thin_tiles != 0);
 }
 
 int sp_conv_fwd(const void* x, int32_t dtype, int64_t n_in, int64_t C, const void* w,

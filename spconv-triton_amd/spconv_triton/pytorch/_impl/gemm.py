@@ -209,6 +209,12 @@ FIRST_USE_MIN_MACS = 2e11
 #: synchronisations): the strided k3 s2 256 -> 256 convolution of 50k uniform
 #: voxels (1.007 pairs per output) 0.56 -> 0.45 ms.
 SURE_PAIRS_PER_ROW = 1.05
+#: Mask-ordered tables whose tiles hold at most THIN_MAX_ITEMS_PER_TILE live
+#: offsets on average (about one pair per row) run the thin kernel, which
+#: loads each reduction chunk three chunks ahead; THIN_TILES forces it on (True)
+#: or off (False) for every ordered call ("auto": by that rule).
+THIN_MAX_ITEMS_PER_TILE = 1.5
+THIN_TILES = "auto"
 _PLAN_MAX_KV = 64  # kv range of the gather plans (sp_gather_plan_bytes)
 _STATS_MAX_KV = 512  # kv range of sp_table_stats
 
@@ -320,9 +326,14 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool 
     if sure or (done > 0 and natural[0] < ORDER_MAX_EFFICIENCY * done):
         order, words = mask_order(pairs, with_words=True)
         perm = permute_table(pairs, order, words if kv <= 32 else None)
-        if sure or mfma_rows(table_stats(perm, n_src)) <= ORDER_MAX_WORK_RATIO * done:
+        masked = table_stats(perm, n_src) if not sure else None
+        if sure or mfma_rows(masked) <= ORDER_MAX_WORK_RATIO * done:
             plan = gather_plan(perm, n_src) if planned else None
             variant = (order, perm, plan)
+            tiles = (M + 255) // 256
+            perm._spconv_triton_thin = (
+                (mode != "mask" and masked is None)  # about one pair per row
+                or (masked is not None and masked[1] <= THIN_MAX_ITEMS_PER_TILE * tiles))
     pairs._spconv_triton_order = (stamp, variant if variant is not None else "natural")
     return variant
 
@@ -414,10 +425,11 @@ def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: 
             variant = key_order_variant(pairs, a.shape[0], plan)
     if variant is not None:
         order, perm, plan = variant
+        thin = THIN_TILES if THIN_TILES != "auto" else getattr(perm, "_spconv_triton_thin", False)
         _lib.check(L.sp_conv_gemm_ordered(
             _lib.ptr(a), _lib.dtype_code(a.dtype), a.shape[0], _lib.ptr(packed), K, kv, C,
             int(transpose), int(bias is not None), _lib.ptr(perm), M, _lib.ptr(order),
-            _lib.ptr(plan), 0 if plan is None else plan.numel(), _lib.ptr(out),
+            _lib.ptr(plan), 0 if plan is None else plan.numel(), int(bool(thin)), _lib.ptr(out),
             _lib.dtype_code(out.dtype), _lib.stream_of(a.device)), "sp_conv_gemm_ordered")
         return
     if plan is not None:

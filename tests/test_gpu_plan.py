@@ -267,35 +267,40 @@ def _orders(a, w, bias, transpose, pairs, M):
 
     N = w.shape[-1] if transpose else w.shape[0]
     outs = {}
-    prev = gemm.ROW_ORDER, gemm.USE_GATHER_PLAN
-    for mode in ("natural", "mask"):
-        for use in (True, False):
-            gemm.ROW_ORDER, gemm.USE_GATHER_PLAN = mode, use
-            try:
-                out = torch.empty((M, N), dtype=a.dtype, device=DEV)
-                gemm._gemm(a, w, bias, transpose, pairs, M, None, None, out)
-                outs[(mode, use)] = out
-            finally:
-                gemm.ROW_ORDER, gemm.USE_GATHER_PLAN = prev
+    prev = gemm.ROW_ORDER, gemm.USE_GATHER_PLAN, gemm.THIN_TILES
+    for mode, use, thin in (("natural", True, "auto"), ("natural", False, "auto"),
+                            ("mask", True, False), ("mask", False, "auto"),
+                            ("mask", True, True)):
+        gemm.ROW_ORDER, gemm.USE_GATHER_PLAN, gemm.THIN_TILES = mode, use, thin
+        try:
+            out = torch.empty((M, N), dtype=a.dtype, device=DEV)
+            gemm._gemm(a, w, bias, transpose, pairs, M, None, None, out)
+            outs[(mode, use) if thin != True else (mode, use, "thin")] = out  # noqa: E712
+        finally:
+            gemm.ROW_ORDER, gemm.USE_GATHER_PLAN, gemm.THIN_TILES = prev
     return outs
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("case", ["subm", "strided", "kv125", "sparse_wide"])
+@pytest.mark.parametrize("case", ["subm", "strided", "kv125", "sparse_wide", "transposed"])
 def test_mask_row_order_bit_identical(case, dtype):
     """Every row sums its offsets in ascending order whatever tile it falls in,
-    so the mask-ordered GEMM (staged, overflow and direct tiles) equals the
+    so the mask-ordered GEMM (staged, overflow and direct tiles, and the thin
+    kernel with the tiles it hands to the direct path) equals the
     natural-order one bit for bit, forward and input gradient."""
     from spconv_triton.pytorch._impl import gemm
 
     rng = np.random.default_rng(44)
     ks, C, K = 3, 32, 48
+    transpose = False
     if case == "subm":
         grid, n, stride = 28, 6000, 1
     elif case == "strided":
         grid, n, stride = 28, 5000, 2
     elif case == "kv125":
         grid, n, stride, ks = 20, 2500, 1, 5
+    elif case == "transposed":  # about one pair per output: thin tiles; 2 column blocks
+        grid, n, stride, C, K, transpose = 30, 800, 2, 48, 96, True
     else:  # wide layer; in mask order 18 of the 47 tiles overflow LDS
         grid, n, stride, C, K = 40, 6000, 1, 136, 128
     idx = rand_indices(rng, 2, [grid] * 3, n)
@@ -304,8 +309,8 @@ def test_mask_row_order_bit_identical(case, dtype):
     from spconv_triton.pytorch import ops
     res = ops.get_indice_pairs_implicit_gemm(torch.from_numpy(idx).to(DEV), 2, [grid] * 3,
                                              ConvAlgo.MaskImplicitGemm, [ks] * 3, [stride] * 3,
-                                             [ks // 2] * 3, [1] * 3, [0] * 3, subm, False,
-                                             is_train=True)
+                                             [0 if transpose else ks // 2] * 3, [1] * 3,
+                                             [0] * 3, subm, transpose, is_train=True)
     pf, pb = res[2], res[3]
     kv = ks ** 3
     torch.manual_seed(3)
@@ -320,6 +325,9 @@ def test_mask_row_order_bit_identical(case, dtype):
         ref = outs[("natural", True)]
         for key, o in outs.items():
             assert torch.equal(o, ref), f"{what} {key} differs from the natural planned GEMM"
+    if case == "transposed":
+        P = int((pf >= 0).sum())
+        assert P <= 1.1 * pf.shape[1], "the case must have about one pair per row"
     if case == "sparse_wide":
         variant = getattr(pf, "_spconv_triton_order")[1]
         plan = variant[2]
