@@ -129,5 +129,9 @@ size_t scan_workspace_bytes(int64_t len);
 // in and out may alias.  total (nullable, device) receives the grand total.
 int exclusive_scan_u32(const uint32_t* in, uint32_t* out, int64_t len, uint32_t* total,
                        void* ws, hipStream_t stream);
+// The same over the population counts of `words` (out[i] = set bits of
+// words[0..i-1]; *total = all set bits); out must not alias words.
+int exclusive_scan_popc(const uint32_t* words, uint32_t* out, int64_t len, uint32_t* total,
+                        void* ws, hipStream_t stream);
 
 }  // namespace sp

@@ -630,12 +630,6 @@ __global__ __launch_bounds__(256) void conv_mark(const int32_t* __restrict__ idx
   wave_count(cnt, npairs);
 }
 
-__global__ __launch_bounds__(256) void popc_words(const uint32_t* __restrict__ bits, int64_t words,
-                                                  uint32_t* __restrict__ out) {
-  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i < words) out[i] = uint32_t(__popc(bits[i]));
-}
-
 // Output row of a marked key.
 __device__ __forceinline__ int64_t bitmap_rank(const uint32_t* __restrict__ bits,
                                                const uint32_t* __restrict__ prefix, uint64_t key) {
@@ -683,6 +677,7 @@ __global__ __launch_bounds__(256) void emit_bitmap_keys(const uint32_t* __restri
   const int64_t w = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (w >= nwords) return;
   uint32_t m = bits[w];
+  if (m == 0) return;  // (sparse volumes: most words; their prefix is not read)
   int64_t r = prefix[w];
   while (m != 0 && r < n_keep) {
     const int b = __ffs(m) - 1;
@@ -1069,11 +1064,8 @@ int sp_pairgen_conv_build(const sp_geom* g, const int32_t* indices, int64_t n, v
     SP_HIP(hipMemsetAsync(npairs, 0, sizeof(unsigned long long), s));
     conv_mark<<<unsigned(cdiv(n, 256)), 256, 0, s>>>(indices, n, d, b.bits, npairs);
     SP_LAUNCHED();
-    const int64_t pbk = cdiv(b.words, 256);
-    SP_CHECK_ARG(pbk <= kMaxGridX, "pairgen: output volume too large");
-    popc_words<<<unsigned(pbk), 256, 0, s>>>(b.bits, b.words, b.prefix);
-    SP_LAUNCHED();
-    rc = exclusive_scan_u32(b.prefix, b.prefix, b.words, b.total, b.scan_ws, s);
+    SP_CHECK_ARG(cdiv(b.words, 256) <= kMaxGridX, "pairgen: output volume too large");
+    rc = exclusive_scan_popc(b.bits, b.prefix, b.words, b.total, b.scan_ws, s);
     if (rc) return rc;
     uint32_t h[34] = {};
     SP_HIP(hipMemcpyAsync(h, b.total, sizeof(h), hipMemcpyDeviceToHost, s));
