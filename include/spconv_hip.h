@@ -160,6 +160,13 @@ int sp_mask_sort(const uint32_t* words, int64_t n, int32_t mic, int32_t kv,
                  uint32_t split_mask, int32_t do_sort, int32_t* pair_mask,
                  int32_t* argsort, void* ws, size_t ws_bytes, void* stream);
 
+/* Positions the radix-sort scatters of this device dropped because they fell
+ * outside 0..n-1 (an inconsistent histogram; 0 unless the library has a bug),
+ * since the process started or the last reset.  Synchronises the device.  No
+ * counterpart in the reference (its sorts are torch's); tests read it after
+ * the sorts they check. */
+int sp_sort_dropped_positions(uint64_t* count, int32_t reset);
+
 /* Per-row compaction of a table [kv, n]: for every k, the columns i with
  * table[k, i] >= 0 in ascending order go to pos_out[k, p] = i and
  * val_out[k, p] = table[k, i]; the tail of each row is filled with -1.

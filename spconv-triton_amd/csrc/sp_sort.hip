@@ -31,6 +31,12 @@ constexpr int kRsSegs = kRsRounds * kRsWaves;  // 32: segment r * kRsWaves + wav
 constexpr int64_t kRsFusedTiles = 128;
 static_assert(kRsTile < 65536, "segment counts are stored as uint16");
 
+// The scatters drop a position outside 0..n-1 instead of writing it (which
+// needs inconsistent histograms, i.e. a bug), and count it here, so a sort
+// that lost items is reported (sp_sort_dropped_positions) rather than leaving
+// holes unnoticed.  One counter per device.
+__device__ unsigned long long g_sort_drops = 0;
+
 struct RowWordDigit {
   const uint32_t* words;
   int mic;
@@ -199,7 +205,10 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter(const Item* __restrict_
     if (idx < n) {
       const uint32_t d = digits[r];
       const uint32_t pos = tile_base[d] + seg[r * kRsWaves + wave][d] + ranks[r];
-      if (pos < uint64_t(n)) out[pos] = items[r];  // always true for consistent counts
+      if (pos < uint64_t(n))
+        out[pos] = items[r];
+      else
+        atomicAdd(&g_sort_drops, 1ull);  // never for consistent counts
     }
   }
 }
@@ -464,7 +473,10 @@ __global__ __launch_bounds__(kRsThreads) void ms_scatter(
     if (idx < n) {
       const uint32_t d = digits[r];
       const uint32_t pos = tile_base[d] + seg[r * kRsWaves + wave][d] + ranks[r];
-      if (pos >= uint64_t(n)) continue;  // never for consistent counts (tests compare the order)
+      if (pos >= uint64_t(n)) {  // never for consistent counts
+        atomicAdd(&g_sort_drops, 1ull);
+        continue;
+      }
       if (kLast) {
         pm_out[pos] = int32_t(keys[r]);
         ar_out[pos] = int32_t(rows[r]);
@@ -542,6 +554,18 @@ static int sort_masks_fused(const uint32_t* words, int64_t n, int kv, uint32_t s
 using namespace sp;
 
 extern "C" {
+
+int sp_sort_dropped_positions(uint64_t* count, int32_t reset) {
+  SP_CHECK_ARG(count, "sort drops: null pointer");
+  unsigned long long v = 0;
+  SP_HIP(hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_sort_drops), sizeof(v)));
+  *count = uint64_t(v);
+  if (reset) {
+    const unsigned long long zero = 0;
+    SP_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_sort_drops), &zero, sizeof(zero)));
+  }
+  return SP_OK;
+}
 
 size_t sp_mask_sort_workspace_size(int64_t n, int32_t mic) {
   const int64_t m = n > 0 ? n : 1;

@@ -101,6 +101,7 @@ _SIGNATURES = {
     "sp_mask_words": (ctypes.c_int, [_P, _I64, _I64, _P, _P]),
     "sp_mask_sort_workspace_size": (_SZ, [_I64, _I32]),
     "sp_mask_sort": (ctypes.c_int, [_P, _I64, _I32, _I32, _U32, _I32, _P, _P, _P, _SZ, _P]),
+    "sp_sort_dropped_positions": (ctypes.c_int, [ctypes.POINTER(ctypes.c_uint64), _I32]),
     "sp_compact_workspace_size": (_SZ, [_I64, _I64]),
     "sp_compact_table": (ctypes.c_int, [_P, _I64, _I64, _P, _P, _P, _P, _I32, _P, _SZ, _P]),
     "sp_native_to_tables": (ctypes.c_int, [_P, _I64, _I64, _I32, _I64, _I64, _P, _P, _P]),

@@ -168,6 +168,7 @@ def test_conv_bitmap_and_hash_paths_bit_exact(gi):
             assert res[2]._spconv_triton_npairs == n_pairs
             if is_train:
                 assert res[3]._spconv_triton_npairs == n_pairs
+    assert _sort_drops() == 0, "a radix-sort scatter dropped positions"
 
 
 @pytest.mark.parametrize("gi", SUBM_GEOMS)
@@ -406,6 +407,20 @@ def test_mask_sort_stable_large(n, grid):
     np.testing.assert_array_equal(res[6][0].cpu().numpy(), exp)
     np.testing.assert_array_equal(res[4][0][:, 0].cpu().numpy().astype(np.int64) & 0xFFFFFFFF,
                                   words[exp])
+    assert _sort_drops() == 0, "a radix-sort scatter dropped positions"
+
+
+def _sort_drops() -> int:
+    """Positions the radix-sort scatters dropped since the last call (0 for
+    consistent histograms), then reset."""
+    import ctypes
+
+    from spconv_triton.pytorch._impl import _lib
+
+    v = ctypes.c_uint64(0)
+    _lib.check(_lib.lib().sp_sort_dropped_positions(ctypes.byref(v), 1),
+               "sp_sort_dropped_positions")
+    return int(v.value)
 
 
 @pytest.mark.parametrize("training", [True, False])
