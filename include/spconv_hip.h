@@ -85,7 +85,8 @@ int sp_geom_key64(const sp_geom* g);
 /* ---- pair generation --------------------------------------------------- */
 
 /* Workspace bytes for sp_pairgen_subm / sp_pairgen_conv_build+fill on n input
- * rows.  The same workspace must be passed, untouched, from build to fill. */
+ * rows.  The same workspace must be passed, untouched, from build to fill; it
+ * must be 16-byte aligned (device allocations are). */
 size_t sp_pairgen_workspace_size(const sp_geom* g, int64_t n);
 
 /* Submanifold rulebook.  pair_fwd [kv, n] (nullable if pair_bwd is given):

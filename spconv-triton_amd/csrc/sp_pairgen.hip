@@ -670,28 +670,47 @@ __global__ __launch_bounds__(256) void conv_fill_bitmap(
 
 // Output coordinates of the kept rows: one thread per bitmap word, its set
 // bits in order (rows prefix[w], prefix[w] + 1, ...).
+// Each thread scans 4 words (one 16-byte load; the bitmap sits at the start of
+// a 256-byte aligned workspace part) and reads the prefix of the non-empty
+// ones only: in a sparse volume almost every word is empty, and one thread
+// per word spent the kernel on workgroup dispatch.
 __global__ __launch_bounds__(256) void emit_bitmap_keys(const uint32_t* __restrict__ bits,
                                                         const uint32_t* __restrict__ prefix,
                                                         int64_t nwords, GeomDev g, int64_t n_keep,
                                                         int32_t* __restrict__ out) {
-  const int64_t w = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (w >= nwords) return;
-  uint32_t m = bits[w];
-  if (m == 0) return;  // (sparse volumes: most words; their prefix is not read)
-  int64_t r = prefix[w];
-  while (m != 0 && r < n_keep) {
-    const int b = __ffs(m) - 1;
-    m &= m - 1u;
-    uint32_t rem = uint32_t(w) * 32u + uint32_t(b);  // bitmap keys are below 2^31
-    int32_t* o = out + r * (g.ndim + 1);
-    for (int d = g.ndim - 1; d >= 0; --d) {
-      const uint32_t sd = uint32_t(g.out_shape[d]);
-      const uint32_t q = rem / sd;
-      o[d + 1] = int32_t(rem - q * sd);
-      rem = q;
+  const int64_t w0 = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+  if (w0 >= nwords) return;
+  uint32_t m4[4];
+  if (w0 + 4 <= nwords) {
+    const uint4 v = *reinterpret_cast<const uint4*>(bits + w0);
+    m4[0] = v.x;
+    m4[1] = v.y;
+    m4[2] = v.z;
+    m4[3] = v.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m4[i] = w0 + i < nwords ? bits[w0 + i] : 0u;
+  }
+  if ((m4[0] | m4[1] | m4[2] | m4[3]) == 0) return;
+  for (int i = 0; i < 4; ++i) {
+    uint32_t m = m4[i];
+    if (m == 0) continue;
+    const int64_t w = w0 + i;
+    int64_t r = prefix[w];
+    while (m != 0 && r < n_keep) {
+      const int b = __ffs(m) - 1;
+      m &= m - 1u;
+      uint32_t rem = uint32_t(w) * 32u + uint32_t(b);  // bitmap keys are below 2^31
+      int32_t* o = out + r * (g.ndim + 1);
+      for (int d = g.ndim - 1; d >= 0; --d) {
+        const uint32_t sd = uint32_t(g.out_shape[d]);
+        const uint32_t q = rem / sd;
+        o[d + 1] = int32_t(rem - q * sd);
+        rem = q;
+      }
+      o[0] = int32_t(rem);
+      ++r;
     }
-    o[0] = int32_t(rem);
-    ++r;
   }
 }
 
@@ -957,6 +976,8 @@ int sp_pairgen_subm(const sp_geom* g, const int32_t* indices, int64_t n, int32_t
   const size_t need = sp_pairgen_workspace_size(g, n);
   if (!ws || ws_bytes < need)
     return set_error(SP_ERR_WORKSPACE, "pairgen_subm: workspace %zu < %zu", ws_bytes, need);
+  SP_CHECK_ARG((reinterpret_cast<uintptr_t>(ws) & 15) == 0,
+               "pairgen_subm: workspace must be 16-byte aligned (its parts take 16-byte accesses)");
   hipStream_t s = as_stream(stream);
   const bool key64 = need_key64(d);
   WsCursor c(ws, ws_bytes);
@@ -1049,6 +1070,8 @@ int sp_pairgen_conv_build(const sp_geom* g, const int32_t* indices, int64_t n, v
   const size_t need = sp_pairgen_workspace_size(g, n);
   if (!ws || ws_bytes < need)
     return set_error(SP_ERR_WORKSPACE, "pairgen_conv_build: workspace %zu < %zu", ws_bytes, need);
+  SP_CHECK_ARG((reinterpret_cast<uintptr_t>(ws) & 15) == 0,
+               "pairgen_conv_build: workspace must be 16-byte aligned (its parts take 16-byte accesses)");
   hipStream_t s = as_stream(stream);
   const bool key64 = need_key64(d);
   WsCursor c(ws, ws_bytes);
@@ -1151,6 +1174,8 @@ int sp_pairgen_conv_fill(const sp_geom* g, const int32_t* indices, int64_t n, co
   const size_t need = sp_pairgen_workspace_size(g, n);
   if (!ws || ws_bytes < need)
     return set_error(SP_ERR_WORKSPACE, "pairgen_conv_fill: workspace %zu < %zu", ws_bytes, need);
+  SP_CHECK_ARG((reinterpret_cast<uintptr_t>(ws) & 15) == 0,
+               "pairgen_conv_fill: workspace must be 16-byte aligned (its parts take 16-byte accesses)");
   SP_CHECK_ARG(n_keep <= conv_bound(d, n), "n_keep exceeds the number of candidate outputs");
   hipStream_t s = as_stream(stream);
   const bool key64 = need_key64(d);
@@ -1167,8 +1192,8 @@ int sp_pairgen_conv_fill(const sp_geom* g, const int32_t* indices, int64_t n, co
                                                             n_keep, pair_fwd, pair_bwd,
                                                             mask_words_bwd, mic);
     SP_LAUNCHED();
-    emit_bitmap_keys<<<unsigned(cdiv(b.words, 256)), 256, 0, s>>>(b.bits, b.prefix, b.words, d,
-                                                                  n_keep, out_indices);
+    emit_bitmap_keys<<<unsigned(cdiv(b.words, 1024)), 256, 0, s>>>(b.bits, b.prefix, b.words, d,
+                                                                   n_keep, out_indices);
     SP_LAUNCHED();
     return SP_OK;
   }
