@@ -25,7 +25,9 @@ weights, and prints one JSON object per configuration:
 * ``ref_c256``: the layer class of the reference's published plots (K3, C256,
   50k voxels in [41, 1600, 1408], batch 1) on uniform voxels: submanifold with
   the rulebook cached, strided and transposed with pair generation, in fp16,
-  fp32 and TF32-equivalent.
+  fp32 and TF32-equivalent;
+* ``wgrad``: the weight gradient of each convolution of the ``resunet``
+  network, one call per layer, with its achieved algorithmic GB/s.
 
 Usage: ``python bench_configs.py [--config NAME ...] [--reps R]``.
 """
@@ -380,9 +382,65 @@ def cfg_ref_c256(reps):
     return out
 
 
+def cfg_wgrad(reps):
+    """The weight gradient of every convolution of the sparse ResUNet training
+    step (config 4, fp16 autocast, 2 x 120k urban voxels): the step runs once
+    with the weight-gradient calls recorded, then each call is timed on its
+    own.  Algorithmic bytes of a call: its pairs' gathered rows,
+    2 * P * (C + K), plus the 8-byte (input row, output row) signal of each
+    pair."""
+    import spconv_triton.pytorch as spconv
+    from spconv_triton.pytorch._impl import gemm as G
+
+    shape = [128, 2048, 2048]
+    idx = urban_cloud(120000, batch=2, seed=9, shape=shape)
+    it = torch.from_numpy(idx).to(DEV)
+    n = idx.shape[0]
+    feats = torch.rand(n, 4, device=DEV)
+    labels = torch.randint(0, 20, (n,), device=DEV)
+    parts = {k: build(v).train() for k, v in RESUNET.items()}
+    head = spconv.SubMConv3d(32, 20, 1, bias=True).to(DEV)
+    join = spconv.JoinTable()
+    calls = []
+    orig = G.conv_backward_weight
+
+    def record(features, grad_out, pair_fwd, weight_shape_krsc, fp32_accum=None):
+        calls.append((features, grad_out, pair_fwd, tuple(weight_shape_krsc)))
+        return orig(features, grad_out, pair_fwd, weight_shape_krsc, fp32_accum)
+
+    G.conv_backward_weight = record
+    try:
+        x = spconv.SparseConvTensor(feats.clone().requires_grad_(True), it, shape, 2)
+        with torch.autocast("cuda", dtype=torch.float16):
+            s0 = parts["stem"](x)
+            s1 = parts["e1"](s0)
+            s2 = parts["e2"](s1)
+            s3 = parts["e3"](s2)
+            u = parts["m2"](join([parts["u3"](s3), s2]))
+            u = parts["m1"](join([parts["u2"](u), s1]))
+            u = parts["m0"](join([parts["u1"](u), s0]))
+            loss = torch.nn.functional.cross_entropy(head(u).features.float(), labels)
+        loss.backward()
+    finally:
+        G.conv_backward_weight = orig
+    layers = []
+    tot_ms = tot_bytes = 0.0
+    for xf, gf, pf, wshape in calls:
+        K, C, kv = wshape[0], wshape[-1], int(pf.shape[0])
+        P = int((pf >= 0).sum().item())
+        ms = _event_ms(lambda: orig(xf, gf, pf, wshape), 5 * reps)
+        nbytes = float(xf.element_size()) * P * (C + K) + 8.0 * P
+        tot_ms += ms
+        tot_bytes += nbytes
+        layers.append({"C": C, "K": K, "kv": kv, "pairs": P, "dtype": str(xf.dtype)[6:],
+                       "ms": round(ms, 4), "GBps": round(nbytes / ms / 1e6, 1)})
+    return {"layers": layers, "total_ms": tot_ms, "total_GBps": round(tot_bytes / tot_ms / 1e6, 1),
+            "frac_of_8TBps": round(tot_bytes / tot_ms / 1e6 / 8000.0, 3)}
+
+
 CONFIGS = {"encoder": cfg_encoder, "resunet": cfg_resunet, "subm4d": cfg_subm4d,
            "wide": cfg_wide, "config1": cfg_config1, "quickstart": cfg_quickstart,
-           "lidar_c256": cfg_lidar_c256, "ref_c256": cfg_ref_c256}
+           "lidar_c256": cfg_lidar_c256, "ref_c256": cfg_ref_c256, "wgrad": cfg_wgrad}
 
 
 def main() -> int:
