@@ -204,7 +204,7 @@ __global__ __launch_bounds__(256) void wgrad_partial(
     const T* __restrict__ X, int64_t n_in, const T* __restrict__ G, int64_t n_out, int C, int K,
     int kv, const int32_t* __restrict__ in_rows, const int32_t* __restrict__ out_rows,
     const int32_t* __restrict__ counts, int64_t stride, int splits, float* __restrict__ part,
-    uint32_t x_bytes, uint32_t g_bytes) {
+    uint32_t x_bytes, uint32_t g_bytes, int cblocks, int nblocks) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
   using S = WgShape<T, BW>;
@@ -228,9 +228,19 @@ __global__ __launch_bounds__(256) void wgrad_partial(
     return COAL ? ((((p >> 3) ^ (((c >> 4) & 1) << 2)) << 3) | (p & 7)) : p;
   };
 
-  const int k = blockIdx.x / splits;
-  const int split = blockIdx.x % splits;
-  const int c0 = blockIdx.y * BW, n0 = blockIdx.z * BW;
+  // (offset, split) pair ks and (c, n) block of this workgroup: the
+  // cblocks * nblocks blocks of one pair gather the same pairs' rows (each
+  // input row for every n block, each gradient row for every c block), so
+  // they run back to back on one XCD (workgroup b runs on XCD b % 8) and the
+  // second reader of a row finds it in that XCD's L2
+  const int bpk = cblocks * nblocks;
+  const int64_t t = blockIdx.x / 8;
+  const int64_t ks = (t / bpk) * 8 + blockIdx.x % 8;
+  if (ks >= int64_t(kv) * splits) return;  // padding of the last group of 8 pairs
+  const int blk = int(t % bpk);
+  const int k = int(ks / splits);
+  const int split = int(ks % splits);
+  const int c0 = (blk / nblocks) * BW, n0 = (blk % nblocks) * BW;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int h = lane >> 5, l32 = lane & 31;
@@ -894,7 +904,10 @@ int sp_conv_wgrad(const void* x, int64_t n_in, const void* g, int64_t n_out, int
   const int vec = (Cg % v == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 ? 1 : 0) |
                   (Kg % v == 0 && reinterpret_cast<uintptr_t>(g) % 16 == 0 ? 2 : 0);
   const int bw = wgrad_block(Cg, Kg);
-  dim3 grid(unsigned(gx), unsigned(cdiv(Cg, bw)), unsigned(cdiv(Kg, bw)));
+  const int cblocks = int(cdiv(Cg, bw)), nblocks = int(cdiv(Kg, bw));
+  const int64_t nwg = 8 * cdiv(gx, 8) * cblocks * nblocks;
+  SP_CHECK_ARG(nwg <= kMaxGridX, "wgrad: grid too large");
+  const dim3 grid{unsigned(nwg), 1u, 1u};
   const int64_t tot = K * kv * C;
   const unsigned rb = unsigned(cdiv(tot, 256));
   auto run = [&](auto tag) {
@@ -907,7 +920,7 @@ int sp_conv_wgrad(const void* x, int64_t n_in, const void* g, int64_t n_out, int
     const Kern kern = bw == 128 ? k128[vec] : k64[vec];
     kern<<<grid, 256, 0, s>>>(static_cast<const T*>(x), n_in, static_cast<const T*>(g), n_out,
                               int(Cg), int(Kg), int(kv), in_rows, out_rows, counts, row_stride,
-                              splits, part, uint32_t(xb), uint32_t(gb));
+                              splits, part, uint32_t(xb), uint32_t(gb), cblocks, nblocks);
     if (split)
       wgrad_reduce_split<<<rb, 256, 0, s>>>(part, splits, K, kv, C, static_cast<float*>(dw));
     else
