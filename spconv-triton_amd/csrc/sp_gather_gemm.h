@@ -149,18 +149,22 @@ __device__ __forceinline__ bool block_tile(int64_t M, int N, int64_t* tile, int*
 // 168 -> 153 us (the 2-D grid, whose column blocks of a tile land on
 // different XCDs, against this one).  Returns false for the padding
 // workgroups past the last tile, which must exit at once.
-__device__ __forceinline__ bool staged_tile(int64_t M, int N, int64_t* tile, int* n0) {
+__device__ __forceinline__ bool staged_tile_of(int64_t b, int64_t nwg, int64_t M, int N,
+                                               int64_t* tile, int* n0) {
   const int gy = (N + 63) / 64;
   if (gy == 1) {
-    *tile = xcd_tile(blockIdx.x, gridDim.x);
+    *tile = xcd_tile(b, nwg);
     *n0 = 0;
     return true;
   }
   const int64_t nt = (M + kTileRows - 1) / kTileRows;
-  const int64_t b = blockIdx.x, x = b % 8, k = b / 8;
+  const int64_t x = b % 8, k = b / 8;
   *tile = (k / gy) * 8 + x;
   *n0 = int(k % gy) * 64;
   return *tile < nt;
+}
+__device__ __forceinline__ bool staged_tile(int64_t M, int N, int64_t* tile, int* n0) {
+  return staged_tile_of(blockIdx.x, gridDim.x, M, N, tile, n0);
 }
 
 // LDS writes of this wave are complete, then the workgroup barrier.  Written
@@ -471,6 +475,132 @@ __device__ __forceinline__ void direct_tile(const T* __restrict__ A, const T* __
   __syncthreads();  // the tables are free for the epilogue
   store_tile<OutT>(acc, bias, ro, smem + L.src_off + uint32_t(wave) * 64u * epi_pitch(sizeof(OutT)),
                    slot0, n0, M, N, lane, order);
+}
+
+// A quarter of a (tile, 64-column block) by the direct path, the whole
+// workgroup: rows 64 q .. 64 q + 63 of the tile, each wave a 32 x 32 block
+// (row half w >> 1, column half w & 1).  A wave holds a quarter of
+// direct_tile's work, so a tile whose waves carry many offsets can be spread
+// over four workgroups.  Same per-row summation order as direct_tile (offset
+// groups, chunks, offsets ascending, then the two K-steps of an item): results
+// are bit-identical.  Uses direct_lds(min(kv, 64) + kPad) bytes of `smem`.
+template <typename T, typename OutT, bool VEC>
+__device__ __forceinline__ void direct_quarter(const T* __restrict__ A, const T* __restrict__ Bt,
+                                               const int32_t* __restrict__ pairs,
+                                               const float* __restrict__ bias,
+                                               OutT* __restrict__ out, const GemmBufs& nb,
+                                               int64_t n_src, int64_t M, int N, int R, int Rp,
+                                               int kv, int64_t tile, int q, int n0,
+                                               unsigned char* smem,
+                                               const int32_t* __restrict__ order) {
+  using frag = typename Mfma<T>::frag;
+  constexpr int V = Mfma<T>::V;
+  constexpr uint32_t ES = sizeof(T);
+  constexpr int kChunk = kChunkBytes / int(ES);  // reduction elements per item
+
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = lane >> 5, l32 = lane & 31;
+  const int64_t slot = tile * kTileRows + q * 64 + (wave >> 1) * 32 + l32;  // this lane's row
+  const bool row_ok = slot < M;
+  const int col = n0 + (wave & 1) * 32 + l32;  // this lane's B / output column
+
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, nb.a_bytes);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bt, nb.bt_bytes);
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(out, nb.out_bytes);
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(pairs, nb.pairs_bytes);
+
+  const int G = kv < kGroupOffsets ? kv : kGroupOffsets;
+  const int E = G + kPad;
+  const DirectLds L = direct_lds(E, uint32_t(sizeof(OutT)));
+  uint32_t* s_kb = reinterpret_cast<uint32_t*>(smem + L.kb_off) + wave * E;
+  int32_t* s_src = reinterpret_cast<int32_t*>(smem + L.src_off) + wave * E * 64;
+
+  const uint32_t row_bytes = uint32_t(R) * ES;
+  const uint32_t slab_bytes = uint32_t(N) * V * ES;        // one (offset, r / V) slab of Bt
+  const uint32_t k_bytes = uint32_t(Rp / V) * slab_bytes;  // one offset of Bt
+  const int nrc = Rp / kChunk;                             // chunks per offset
+  const uint32_t bcol = col < N ? uint32_t(col) * V * ES : kColOob;
+
+  floatx16 acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  for (int kc = 0; kc < kv; kc += G) {
+    const int kn = kv - kc < G ? kv - kc : G;
+    __syncthreads();  // the previous group's tables are no longer read
+    // ---- this wave's table of the offsets with a pair in its 32 rows
+    int nact = 0;
+    constexpr int kTabBatch = 16;  // table loads in flight per lane
+    for (int u0 = 0; u0 < kn; u0 += kTabBatch) {
+      int32_t v[kTabBatch];
+#pragma unroll
+      for (int u = 0; u < kTabBatch; ++u) {
+        const bool in = row_ok && u0 + u < kn;
+        const int64_t e = int64_t(kc + u0 + u) * M + slot;
+        v[u] = int32_t(__builtin_amdgcn_raw_buffer_load_b32(rp, in ? uint32_t(e * 4) : kOob, 0, 0));
+      }
+#pragma unroll
+      for (int u = 0; u < kTabBatch; ++u) {
+        const bool ok = row_ok && u0 + u < kn && v[u] >= 0 && v[u] < n_src;
+        if (u0 + u < kn && __ballot(ok)) {  // wave-uniform (both lane halves hold the same rows)
+          if (h == 0) s_src[nact * 32 + l32] = ok ? v[u] : -1;
+          if (lane == 0) s_kb[nact] = uint32_t(kc + u0 + u) * k_bytes;
+          ++nact;
+        }
+      }
+    }
+#pragma unroll
+    for (int pi = 0; pi < kPad; ++pi) {  // padding items: no source row, out-of-range B
+      if (h == 0) s_src[(nact + pi) * 32 + l32] = -1;
+      if (lane == 0) s_kb[nact + pi] = kBOob;
+    }
+    for (int rc = 0; rc < nrc; ++rc) {
+      auto load = [&](int it, frag (&a)[2], frag (&b)[2]) {
+        const int32_t src = s_src[it * 32 + l32];
+        const uint32_t kb = s_kb[it];
+        const uint32_t base = src >= 0 ? uint32_t(src) * row_bytes : kOob;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const int e0 = rc * kChunk + (ks * 2 + h) * V;
+          if (VEC)
+            a[ks] = buf_frag<T>(ra, (base != kOob && e0 < R) ? base + uint32_t(e0) * ES : kOob);
+          else
+            a[ks] = buf_frag_elems<T>(ra, base, e0, R);
+          b[ks] = buf_frag<T>(rb, kb + bcol + uint32_t(rc * 4 + ks * 2 + h) * slab_bytes);
+        }
+      };
+      // two items in flight: item it + 2 loads while item it multiplies
+      frag a0[2], b0[2], a1[2], b1[2], a2[2], b2[2];
+      load(0, a0, b0);
+      load(1, a1, b1);
+      auto step = [&](int it, frag (&ac)[2], frag (&bc)[2], frag (&an)[2], frag (&bn)[2]) {
+        load(it + 2, an, bn);
+        __builtin_amdgcn_sched_barrier(0);
+        Mfma<T>::mma(ac[0], bc[0], acc);
+        Mfma<T>::mma(ac[1], bc[1], acc);
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      for (int it = 0; it < nact; it += 3) {  // reads entries up to nact + 4 < nact + kPad
+        step(it, a0, b0, a2, b2);
+        step(it + 1, a1, b1, a0, b0);
+        step(it + 2, a2, b2, a1, b1);
+      }
+    }
+  }
+  // ---- epilogue: element stores (+ bias); rows past M and columns past N dropped
+  const float bv = (bias && col < N) ? bias[col] : 0.f;
+  auto out_row = [&](int64_t s) -> int64_t {
+    if (!order || s >= M) return s;
+    const int64_t r = order[s];
+    return (r >= 0 && r < M) ? r : M;
+  };
+  const int64_t r0 = tile * kTileRows + q * 64 + (wave >> 1) * 32;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int64_t row = out_row(r0 + 8 * (i / 4) + 4 * h + (i % 4));
+    const uint32_t off = (row < M && col < N) ? uint32_t((row * N + col) * int64_t(sizeof(OutT)))
+                                              : kOob;
+    buf_store<OutT>(from_f32<OutT>(acc[i] + bv), ro, off);
+  }
 }
 
 // Every tile of an unplanned call, one workgroup per (tile, 64 columns).
@@ -832,6 +962,23 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
 
 constexpr int kThinRows = 320;   // staged rows per tile, including the zero row
 constexpr int kThinItems = 4;    // items a thin tile may hold
+// The thin kernel's QUARTER instances take the direct path in quarters
+// (direct_quarter) and spread those of the last kThinSplitTiles tiles over
+// four workgroups.  The host picks them for fp32 operands (whose MFMAs are
+// slow enough that a wave of a heavy tile sets the kernel's end) and for
+// 16-bit grids of at most kThinQuarterGrid workgroups (where the heavy tiles'
+// waves run after most others are done); elsewhere a quarter's 32 x 32 waves,
+// which load twice the bytes per MFMA of direct_tile's 64 x 64 ones, cost
+// more than the split saves.  The two paths are never compiled into one
+// instance: together they outgrow the instruction cache.
+constexpr int kThinSplitTiles = 16;
+constexpr int64_t kThinQuarterGrid = 1024;
+
+// Workgroups in front of the thin grid for quarters 1..3 of the last n_split
+// tiles' gy column blocks, rounded up to 8 so that the XCD mapping holds.
+__host__ __device__ inline int64_t thin_split_extra(int n_split, int gy) {
+  return 8 * ((3 * int64_t(n_split) * gy + 7) / 8);
+}
 
 struct ThinLds {
   uint32_t rows_off, slab_off, total;
@@ -846,12 +993,12 @@ __host__ __device__ inline ThinLds thin_lds(uint32_t out_size) {
   return l;
 }
 
-template <typename T, typename OutT, bool VEC, bool ORDERED>
+template <typename T, typename OutT, bool VEC, bool ORDERED, bool QUARTER>
 __global__ __launch_bounds__(256, 2) void gather_gemm_thin(
     const T* __restrict__ A, const T* __restrict__ Bt, const int32_t* __restrict__ pairs,
     const int32_t* __restrict__ order_arg, PlanDev plan, const float* __restrict__ bias,
     OutT* __restrict__ out, GemmBufs nb, int64_t n_src, int64_t M, int N, int R, int Rp,
-    int kv) {
+    int kv, int n_split) {
   const int32_t* __restrict__ order = ORDERED ? order_arg : nullptr;
   using frag = typename Mfma<T>::frag;
   constexpr int V = Mfma<T>::V;
@@ -865,21 +1012,61 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_thin(
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int h = lane >> 5, l32 = lane & 31;
+  // Tiles the thin layout does not hold (the rows with the most mask bits,
+  // last in mask order) take the direct path, and their waves carry many
+  // offsets.  QUARTER instances: among the last n_split tiles each such (tile,
+  // 64-column block) is spread over four workgroups of a quarter of its rows:
+  // the grid's first n_extra workgroups (3 per (tile, column block) of those
+  // tiles, rounded up to 8 so that the XCD mapping below holds) take quarters
+  // 1..3 and exit at once for other tiles; the rest take the tiles as below,
+  // with quarter 0 of a split tile and all four quarters of an earlier one.
   int64_t tile;
   int n0;
-  if (!staged_tile(M, N, &tile, &n0)) return;
-  // tiles in reverse order: in mask order the rows with the most bits come
-  // last, and their tiles (the ones the direct path takes, many times longer
-  // than a thin one) should start first rather than set the kernel's end
-  tile = (M + kTileRows - 1) / kTileRows - 1 - tile;
+  if constexpr (QUARTER) {
+    const int64_t nt_all = (M + kTileRows - 1) / kTileRows;
+    const int gy = (N + 63) / 64;
+    const int64_t n_extra = thin_split_extra(n_split, gy);
+    auto direct_heavy = [&](int64_t t) -> bool {
+      return plan.count[t] >= kThinRows || plan.nact[t] > kThinItems;
+    };
+    int q_lo = 0, q_hi = 0;  // quarters [q_lo, q_hi) by the direct path
+    if (blockIdx.x < n_extra) {
+      const int64_t e = blockIdx.x;
+      if (e >= 3 * n_split * gy) return;
+      const int64_t tc = e / 3;  // (tile, column block), heaviest tiles first
+      tile = nt_all - 1 - tc / gy;
+      if (!direct_heavy(tile)) return;
+      n0 = int(tc % gy) * 64;
+      q_lo = 1 + int(e % 3);
+      q_hi = q_lo + 1;
+    } else {
+      if (!staged_tile_of(blockIdx.x - n_extra, gridDim.x - n_extra, M, N, &tile, &n0)) return;
+      tile = nt_all - 1 - tile;  // reverse order, as below
+      if (direct_heavy(tile)) q_hi = tile >= nt_all - n_split ? 1 : 4;
+    }
+    if (q_hi > 0) {  // whole workgroup (uniform)
+      for (int qr = q_lo; qr < q_hi; ++qr)
+        direct_quarter<T, OutT, VEC>(A, Bt, pairs, bias, out, nb, n_src, M, N, R, Rp, kv, tile,
+                                     qr, n0, smem, order);
+      return;
+    }
+  } else {
+    if (!staged_tile(M, N, &tile, &n0)) return;
+    // tiles in reverse order: in mask order the rows with the most bits come
+    // last, and their tiles (the ones the direct path takes, many times
+    // longer than a thin one) should start first rather than set the end
+    tile = (M + kTileRows - 1) / kTileRows - 1 - tile;
+  }
   const int64_t slot0 = tile * kTileRows + wave * 64;
 
   const int U = plan.count[tile];
   const int nact = plan.nact[tile];
-  if (U >= kThinRows || nact > kThinItems) {  // whole workgroup (uniform)
-    direct_tile<T, OutT, VEC>(A, Bt, pairs, bias, out, nb, n_src, M, N, R, Rp, kv, tile, n0, smem,
-                              order);
-    return;
+  if constexpr (!QUARTER) {
+    if (U >= kThinRows || nact > kThinItems) {  // whole workgroup (uniform)
+      direct_tile<T, OutT, VEC>(A, Bt, pairs, bias, out, nb, n_src, M, N, R, Rp, kv, tile, n0,
+                                smem, order);
+      return;
+    }
   }
 
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, nb.a_bytes);

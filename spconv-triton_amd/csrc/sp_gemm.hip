@@ -588,14 +588,23 @@ template <typename T, typename OutT, bool VEC>
 static int launch_thin(dim3 grid, hipStream_t s, const T* A, const T* bt, const int32_t* pairs,
                        OutT* o, GemmBufs nb, const GemmCall& c) {
   const uint32_t lds = thin_kernel_lds(c.kv, uint32_t(sizeof(OutT)));
-  auto kern = c.order ? gather_gemm_thin<T, OutT, VEC, true> : gather_gemm_thin<T, OutT, VEC, false>;
-  static bool attr_set[2] = {false, false};  // per kernel instance
+  const bool quarter = sizeof(T) == 4 || grid.x <= kThinQuarterGrid;
+  auto kern = quarter ? (c.order ? gather_gemm_thin<T, OutT, VEC, true, true>
+                                 : gather_gemm_thin<T, OutT, VEC, false, true>)
+                      : (c.order ? gather_gemm_thin<T, OutT, VEC, true, false>
+                                 : gather_gemm_thin<T, OutT, VEC, false, false>);
+  static bool attr_set[4] = {false, false, false, false};  // per kernel instance
   int rc = allow_lds(reinterpret_cast<const void*>(kern),
                      thin_kernel_lds(kPlanMaxKv, uint32_t(sizeof(OutT))),
-                     attr_set[c.order ? 1 : 0]);
+                     attr_set[(c.order ? 1 : 0) + (quarter ? 2 : 0)]);
   if (rc) return rc;
+  const int64_t nt = cdiv(c.M, kTileRows);
+  const int n_split = quarter ? int(nt < kThinSplitTiles ? nt : kThinSplitTiles) : 0;
+  const int64_t n_extra = thin_split_extra(n_split, int(cdiv(c.N, 64)));
+  SP_CHECK_ARG(n_extra + grid.x <= kMaxGridX, "gemm: too many tiles");
+  grid.x = unsigned(n_extra + grid.x);
   kern<<<grid, 256, lds, s>>>(A, bt, pairs, c.order, c.plan, c.bias, o, nb, c.n_src, c.M, c.N,
-                              c.R, c.Rp, c.kv);
+                              c.R, c.Rp, c.kv, n_split);
   SP_LAUNCHED();
   return SP_OK;
 }

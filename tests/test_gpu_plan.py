@@ -282,12 +282,16 @@ def _orders(a, w, bias, transpose, pairs, M):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("case", ["subm", "strided", "kv125", "sparse_wide", "transposed"])
+@pytest.mark.parametrize("case", ["subm", "strided", "kv125", "sparse_wide", "transposed",
+                                  "subm_long"])
 def test_mask_row_order_bit_identical(case, dtype):
     """Every row sums its offsets in ascending order whatever tile it falls in,
     so the mask-ordered GEMM (staged, overflow and direct tiles, and the thin
-    kernel with the tiles it hands to the direct path) equals the
-    natural-order one bit for bit, forward and input gradient."""
+    kernel with the tiles it hands to the direct path, whole or in quarters)
+    equals the natural-order one bit for bit, forward and input gradient.
+    subm_long: a forward grid of 1 175 workgroups (5 column blocks), where the
+    16-bit thin kernel gives its direct tiles to direct_tile, and a dgrad grid
+    of 235, where it splits them into quarters."""
     from spconv_triton.pytorch._impl import gemm
 
     rng = np.random.default_rng(44)
@@ -299,6 +303,8 @@ def test_mask_row_order_bit_identical(case, dtype):
         grid, n, stride = 28, 5000, 2
     elif case == "kv125":
         grid, n, stride, ks = 20, 2500, 1, 5
+    elif case == "subm_long":
+        grid, n, stride, C, K = 48, 60000, 1, 32, 320
     elif case == "transposed":  # about one pair per output: thin tiles; 2 column blocks
         grid, n, stride, C, K, transpose = 30, 800, 2, 48, 96, True
     else:  # wide layer; in mask order 18 of the 47 tiles overflow LDS
