@@ -150,3 +150,52 @@ def test_tf32_module_training_step():
         scale = float(b.abs().max())
         assert float((a - b).abs().max()) <= 1e-3 * max(scale, 1e-6)
     assert not torch.equal(res[True][0], res[False][0])
+
+
+def test_fp16_accumulation_flags_served_at_fp32():
+    """SPCONV_ALLOW_FP16_ACCUM / fp32_accum=False (reference _impl/gemm.py:456-498)
+    ask for fp16 accumulation, which gfx950's MFMAs do not offer: the flags are
+    accepted and the GEMMs accumulate in fp32, so the results equal the
+    default ones bit for bit (forward, input gradient and weight gradient in
+    fp16, through the GEMM wrappers and through a module training step)."""
+    import spconv_triton.pytorch as spconv
+    from spconv_triton import constants
+    from spconv_triton.pytorch._impl import gemm
+
+    rng = np.random.default_rng(8)
+    idx = rand_indices(rng, 2, [24] * 3, 3000)
+    res = _tables(idx, 2, [24] * 3, [3] * 3, [1] * 3, [1] * 3, True)
+    pf, pb = res[2], res[3]
+    torch.manual_seed(5)
+    x = torch.randn(idx.shape[0], 32, device=DEV).half()
+    g = torch.randn(pf.shape[1], 48, device=DEV).half()
+    w = (torch.randn(48, 3, 3, 3, 32, device=DEV) / 30).half()
+    n = idx.shape[0]
+    for acc in (None, True):
+        assert torch.equal(gemm.conv_forward(x, w, pf, n, fp32_accum=False),
+                           gemm.conv_forward(x, w, pf, n, fp32_accum=acc))
+        assert torch.equal(gemm.conv_backward_input(g, w, pb, n, fp32_accum=False),
+                           gemm.conv_backward_input(g, w, pb, n, fp32_accum=acc))
+        assert torch.equal(gemm.conv_backward_weight(x, g, pf, w.shape, fp32_accum=False),
+                           gemm.conv_backward_weight(x, g, pf, w.shape, fp32_accum=acc))
+
+    t = torch.from_numpy(idx).to(DEV)
+    torch.manual_seed(6)
+    net = spconv.SparseSequential(spconv.SubMConv3d(32, 48, 3, padding=1, indice_key="s"),
+                                  spconv.SparseConv3d(48, 16, 3, stride=2, padding=1))
+    net = net.to(DEV).half().train()
+    out = {}
+    prev = constants.SPCONV_ALLOW_FP16_ACCUM
+    try:
+        for flag in (False, True):
+            constants.SPCONV_ALLOW_FP16_ACCUM = flag
+            net.zero_grad()
+            f = x.clone().requires_grad_(True)
+            y = net(spconv.SparseConvTensor(f, t, [24] * 3, 2))
+            y.features.float().square().sum().backward()
+            out[flag] = [y.features.clone(), f.grad.clone()] + [p.grad.clone()
+                                                                 for p in net.parameters()]
+    finally:
+        constants.SPCONV_ALLOW_FP16_ACCUM = prev
+    for a, b in zip(out[True], out[False]):
+        assert torch.equal(a, b)
