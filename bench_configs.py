@@ -11,9 +11,10 @@ weights, and prints one JSON object per configuration:
   autocast, batch 2 x ~120k voxels in [128, 2048, 2048]; rulebooks rebuilt
   every step;
 * ``subm4d``: SubMConv4d 3^4, 128 -> 128 fp16, ~500k voxels in
-  [64, 512, 512, 512], rulebook cached;
+  [64, 512, 512, 512], rulebook cached, with its pairs per row and the
+  matrix-core utilisation (useful flop 2 * pairs * C * K);
 * ``wide``: SubMConv3d 256 -> 256 fp16, 400k voxels of a 1024^3 surface
-  cloud, rulebook cached;
+  cloud, rulebook cached, with the same two figures;
 * ``config1``: SubMConv3d 16 -> 16 fp32, 2,000 uniform voxels in 64^3,
   rulebook rebuilt every pass (the reference's CPU-runnable case);
 * ``quickstart``: the reference README chain SubMConv3d(3 -> 32) ->
@@ -180,6 +181,11 @@ def _cached_layer(conv, idx, shape, C, reps):
     bs = int(idx[:, 0].max()) + 1
     with torch.no_grad():
         y = conv(spconv.SparseConvTensor(feats, it, shape, bs))
+        rb = y.indice_dict[conv.indice_key]
+        if getattr(rb, "pair_fwd", None) is not None:  # implicit-GEMM rulebook
+            pairs = int((rb.pair_fwd >= 0).sum().item())
+        else:  # Native rulebook: per-offset pair counts
+            pairs = int(rb.indice_pair_num.sum().item())
         xc = spconv.SparseConvTensor(feats, it, shape, bs, indice_dict=y.indice_dict)
         for _ in range(5):
             conv(xc)
@@ -191,7 +197,15 @@ def _cached_layer(conv, idx, shape, C, reps):
             conv(xc)
         e1.record()
         torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / n
+    return e0.elapsed_time(e1) / n, pairs
+
+
+def _mfma_report(ms, pairs, n, C, K):
+    """Useful matrix-core work of a layer: 2 * pairs * C * K flop over its time,
+    as a fraction of the fp16 dense peak (2.5 PFLOP/s)."""
+    tflops = 2.0 * pairs * C * K / (ms * 1e-3) / 1e12
+    return {"pairs_per_row": round(pairs / n, 3), "useful_tflops": round(tflops, 1),
+            "matrix_core_frac": round(tflops / 2500.0, 4), "peak_used": "fp16 2.5 PFLOP/s"}
 
 
 def cfg_subm4d(reps):
@@ -209,8 +223,9 @@ def cfg_subm4d(reps):
     idx = np.unique(np.concatenate(rows).astype(np.int32), axis=0)
     torch.manual_seed(0)
     conv = spconv.SubMConv4d(128, 128, 3, padding=1, bias=False, indice_key="k").to(DEV)
-    ms = _cached_layer(conv.half().eval(), idx, [64, 512, 512, 512], 128, reps)
+    ms, pairs = _cached_layer(conv.half().eval(), idx, [64, 512, 512, 512], 128, reps)
     return {"voxels": int(idx.shape[0]), "median_ms": ms,
+            **_mfma_report(ms, pairs, int(idx.shape[0]), 128, 128),
             "what": "SubMConv4d 3^4 128->128 fp16 forward, rulebook cached (mean)"}
 
 
@@ -220,8 +235,9 @@ def cfg_wide(reps):
     idx = surface_cloud(400000, 1024, seed=0)
     torch.manual_seed(0)
     conv = spconv.SubMConv3d(256, 256, 3, padding=1, bias=False, indice_key="k").to(DEV)
-    ms = _cached_layer(conv.half().eval(), idx, [1024] * 3, 256, reps)
+    ms, pairs = _cached_layer(conv.half().eval(), idx, [1024] * 3, 256, reps)
     return {"voxels": int(idx.shape[0]), "median_ms": ms,
+            **_mfma_report(ms, pairs, int(idx.shape[0]), 256, 256),
             "what": "SubMConv3d 256->256 fp16 forward, 1024^3 surface cloud, rulebook cached (mean)"}
 
 

@@ -248,11 +248,18 @@ int sp_conv_gemm_planned(const void* a, int32_t dtype, int64_t n_src, const void
  * reads it coalesced.  thin_tiles != 0 (with a plan): most tiles of
  * pairs_perm hold at most 4 live offsets (tables of about one pair per row);
  * a kernel that loads each chunk's rows and weights three chunks ahead runs
- * them (the others take the direct path inside it).  Results are the same. */
+ * them (the others take the direct path inside it).  Results are the same.
+ * row_words (nullable): the mask words of pairs_perm's rows, words_per_row
+ * (>= ceil(kv / 32)) per row (bit k of row i set iff pairs_perm[k, i] >= 0,
+ * e.g. the sorted pair_mask of sp_mask_sort whose argsort is row_order); an
+ * unplanned call then reads the table entries of only the offsets set in a
+ * wave's rows (tables with few pairs per row and kv > 64 gain most).  A clear
+ * bit whose entry holds a pair drops that pair. */
 int sp_conv_gemm_ordered(const void* a, int32_t dtype, int64_t n_src, const void* packed,
                          int64_t K, int64_t kv, int64_t C, int32_t transpose, int32_t has_bias,
                          const int32_t* pairs_perm, int64_t M, const int32_t* row_order,
-                         const void* plan, size_t plan_bytes, int32_t thin_tiles, void* out,
+                         const void* plan, size_t plan_bytes, int32_t thin_tiles,
+                         const uint32_t* row_words, int32_t words_per_row, void* out,
                          int32_t out_dtype, void* stream);
 
 /* out[k, i] = pairs[k, order[i]] for a gather table pairs [kv, M] (-1 where

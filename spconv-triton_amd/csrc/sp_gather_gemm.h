@@ -328,7 +328,10 @@ __host__ __device__ inline DirectLds direct_lds(int E, uint32_t out_size) {
 // One (tile, 64-column block) of the direct kernel, the whole workgroup:
 // every tile of an unplanned call, and the tiles of a planned call whose
 // distinct rows do not fit in LDS.  Uses direct_lds(min(kv, 64) + kPad) bytes
-// of `smem`.
+// of `smem`.  words (nullable): the mask words of the table's rows, `mic` per
+// row (bit k of row r set iff pairs[k, r] >= 0); with them a wave reads the
+// table entries of only the offsets set in its rows' masks, instead of all kv
+// (the items found, and so the result, are the same).
 template <typename T, typename OutT, bool VEC>
 __device__ __forceinline__ void direct_tile(const T* __restrict__ A, const T* __restrict__ Bt,
                                             const int32_t* __restrict__ pairs,
@@ -336,7 +339,9 @@ __device__ __forceinline__ void direct_tile(const T* __restrict__ A, const T* __
                                             OutT* __restrict__ out, const GemmBufs& nb,
                                             int64_t n_src, int64_t M, int N, int R, int Rp,
                                             int kv, int64_t tile, int n0, unsigned char* smem,
-                                            const int32_t* __restrict__ order) {
+                                            const int32_t* __restrict__ order,
+                                            const uint32_t* __restrict__ words = nullptr,
+                                            int mic = 0) {
   using frag = typename Mfma<T>::frag;
   constexpr int V = Mfma<T>::V;
   constexpr uint32_t ES = sizeof(T);
@@ -378,21 +383,66 @@ __device__ __forceinline__ void direct_tile(const T* __restrict__ A, const T* __
     // ---- per-wave tables of the offsets with a pair in this wave's 64 rows
     int nact = 0;
     constexpr int kTabBatch = 16;  // table loads in flight per lane
-    for (int u0 = 0; u0 < kn; u0 += kTabBatch) {
-      int32_t v[kTabBatch];
-#pragma unroll
-      for (int u = 0; u < kTabBatch; ++u) {
-        const bool in = row_ok && u0 + u < kn;
-        const int64_t e = int64_t(kc + u0 + u) * M + my_row;
-        v[u] = int32_t(__builtin_amdgcn_raw_buffer_load_b32(rp, in ? uint32_t(e * 4) : kOob, 0, 0));
+    if (words) {
+      // the offsets kc .. kc + kn - 1 set in any of the wave's rows' masks
+      // (kc is a multiple of 64, so they are bits of words kc / 32 and the next)
+      uint32_t m_lo = 0u, m_hi = 0u;
+      if (row_ok) {
+        const int w0 = kc >> 5;
+        const uint32_t* wr = words + my_row * int64_t(mic);
+        m_lo = w0 < mic ? wr[w0] : 0u;
+        m_hi = w0 + 1 < mic ? wr[w0 + 1] : 0u;
       }
 #pragma unroll
-      for (int u = 0; u < kTabBatch; ++u) {
-        const bool ok = row_ok && u0 + u < kn && v[u] >= 0 && v[u] < n_src;
-        if (u0 + u < kn && __ballot(ok)) {  // wave-uniform
-          s_src[(nact * 32 + l32) * 2 + h] = ok ? v[u] : -1;  // [item][l32][mt], mt = lane / 32
-          if (lane == 0) s_kb[nact] = uint32_t(kc + u0 + u) * k_bytes;
-          ++nact;
+      for (int off = 32; off > 0; off >>= 1) {
+        m_lo |= __shfl_xor(m_lo, off, 64);
+        m_hi |= __shfl_xor(m_hi, off, 64);
+      }
+      uint64_t live = (uint64_t(m_hi) << 32) | m_lo;  // wave-uniform
+      if (kn < 64) live &= (uint64_t(1) << kn) - 1u;
+      while (live) {  // a batch of the lowest set offsets, ascending
+        int us[kTabBatch];
+#pragma unroll
+        for (int b = 0; b < kTabBatch; ++b) {
+          us[b] = live ? int(__builtin_ctzll(live)) : -1;
+          live &= live ? live - 1u : uint64_t(0);
+        }
+        int32_t v[kTabBatch];
+#pragma unroll
+        for (int b = 0; b < kTabBatch; ++b) {
+          const bool in = row_ok && us[b] >= 0;
+          const int64_t e = int64_t(kc + (us[b] >= 0 ? us[b] : 0)) * M + my_row;
+          v[b] = int32_t(
+              __builtin_amdgcn_raw_buffer_load_b32(rp, in ? uint32_t(e * 4) : kOob, 0, 0));
+        }
+#pragma unroll
+        for (int b = 0; b < kTabBatch; ++b) {
+          const bool ok = row_ok && us[b] >= 0 && v[b] >= 0 && v[b] < n_src;
+          if (us[b] >= 0 && __ballot(ok)) {  // wave-uniform
+            s_src[(nact * 32 + l32) * 2 + h] = ok ? v[b] : -1;
+            if (lane == 0) s_kb[nact] = uint32_t(kc + us[b]) * k_bytes;
+            ++nact;
+          }
+        }
+      }
+    } else {
+      for (int u0 = 0; u0 < kn; u0 += kTabBatch) {
+        int32_t v[kTabBatch];
+#pragma unroll
+        for (int u = 0; u < kTabBatch; ++u) {
+          const bool in = row_ok && u0 + u < kn;
+          const int64_t e = int64_t(kc + u0 + u) * M + my_row;
+          v[u] = int32_t(
+              __builtin_amdgcn_raw_buffer_load_b32(rp, in ? uint32_t(e * 4) : kOob, 0, 0));
+        }
+#pragma unroll
+        for (int u = 0; u < kTabBatch; ++u) {
+          const bool ok = row_ok && u0 + u < kn && v[u] >= 0 && v[u] < n_src;
+          if (u0 + u < kn && __ballot(ok)) {  // wave-uniform
+            s_src[(nact * 32 + l32) * 2 + h] = ok ? v[u] : -1;  // [item][l32][mt], mt = lane / 32
+            if (lane == 0) s_kb[nact] = uint32_t(kc + u0 + u) * k_bytes;
+            ++nact;
+          }
         }
       }
     }
@@ -610,13 +660,14 @@ template <typename T, typename OutT, bool VEC, bool ORDERED>
 __global__ __launch_bounds__(256, 2) void gather_gemm_direct(
     const T* __restrict__ A, const T* __restrict__ Bt, const int32_t* __restrict__ pairs,
     const int32_t* __restrict__ order, const float* __restrict__ bias, OutT* __restrict__ out,
-    GemmBufs nb, int64_t n_src, int64_t M, int N, int R, int Rp, int kv) {
+    GemmBufs nb, int64_t n_src, int64_t M, int N, int R, int Rp, int kv,
+    const uint32_t* __restrict__ words, int mic) {
   extern __shared__ __align__(16) unsigned char smem[];
   int64_t tile;
   int n0;
   if (!block_tile(M, N, &tile, &n0)) return;
   direct_tile<T, OutT, VEC>(A, Bt, pairs, bias, out, nb, n_src, M, N, R, Rp, kv, tile, n0, smem,
-                            ORDERED ? order : nullptr);
+                            ORDERED ? order : nullptr, ORDERED ? words : nullptr, mic);
 }
 
 // ---------------------------------------------------------------------------

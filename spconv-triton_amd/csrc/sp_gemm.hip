@@ -518,6 +518,8 @@ struct GemmCall {
   PlanDev plan;
   const float* bias;
   const int32_t* order;  // tile row -> output row, or null (natural order)
+  const uint32_t* words;  // ordered direct kernel: the rows' mask words (nullable), mic per row
+  int mic;
   bool vec;
   bool thin;             // planned: the thin kernel (tiles of at most kThinItems items)
 };
@@ -544,7 +546,7 @@ static int launch_direct(dim3 grid, hipStream_t s, const T* A, const T* bt, cons
                      attr_set[c.order ? 1 : 0]);
   if (rc) return rc;
   kern<<<grid, 256, lds, s>>>(A, bt, pairs, c.order, c.bias, o, nb, c.n_src, c.M, c.N, c.R, c.Rp,
-                              c.kv);
+                              c.kv, c.words, c.mic);
   SP_LAUNCHED();
   return SP_OK;
 }
@@ -678,12 +680,15 @@ static int gemm_packed(const void* A, int dtype, int64_t n_src, const void* pack
                        int64_t kv, int64_t C, int transpose, int has_bias, const int32_t* pairs,
                        int64_t M, const int32_t* pm, const int32_t* ar, const void* plan,
                        size_t plan_bytes, void* out, int out_dtype, hipStream_t s,
-                       const int32_t* order = nullptr, bool thin = false) {
+                       const int32_t* order = nullptr, bool thin = false,
+                       const uint32_t* words = nullptr, int mic = 0) {
   SP_CHECK_ARG(gemm_dtype_ok(dtype), "gemm: feature dtype %d not supported (f16/bf16/f32)", dtype);
   SP_CHECK_ARG(K >= 1 && C >= 1 && kv >= 1 && M >= 0 && n_src >= 0, "gemm: bad sizes");
   SP_CHECK_ARG(K < 65536 && C < 65536 && kv < 65536, "gemm: channel/kernel size too large");
   SP_CHECK_ARG(!((pm == nullptr) ^ (ar == nullptr)), "gemm: pair_mask and argsort go together");
   SP_CHECK_ARG(!(pm && kv > 32), "gemm: masked path needs kv <= 32");
+  SP_CHECK_ARG(!words || (order && mic >= (kv + 31) / 32 && mic <= 1024),
+               "gemm: row mask words need a row order and >= ceil(kv/32) words per row (%d)", mic);
   if (M == 0) return SP_OK;
   SP_CHECK_ARG(A && packed && pairs && out, "gemm: null pointer");
   const Packed p = packed_layout(K, kv, C, dtype, transpose);
@@ -697,6 +702,8 @@ static int gemm_packed(const void* A, int dtype, int64_t n_src, const void* pack
   c.kv = int(kv);
   c.bias = has_bias ? reinterpret_cast<const float*>(base + p.bias_off) : nullptr;
   c.order = order;
+  c.words = words;
+  c.mic = words ? mic : 0;
   c.vec = (p.R % vec_of(dtype) == 0) && (reinterpret_cast<uintptr_t>(A) % 16 == 0);
   c.planned = plan != nullptr;
   c.thin = thin && plan != nullptr;
@@ -830,12 +837,13 @@ int sp_conv_gemm_planned(const void* a, int32_t dtype, int64_t n_src, const void
 int sp_conv_gemm_ordered(const void* a, int32_t dtype, int64_t n_src, const void* packed,
                          int64_t K, int64_t kv, int64_t C, int32_t transpose, int32_t has_bias,
                          const int32_t* pairs_perm, int64_t M, const int32_t* row_order,
-                         const void* plan, size_t plan_bytes, int32_t thin_tiles, void* out,
+                         const void* plan, size_t plan_bytes, int32_t thin_tiles,
+                         const uint32_t* row_words, int32_t words_per_row, void* out,
                          int32_t out_dtype, void* stream) {
   SP_CHECK_ARG(row_order != nullptr, "gemm: null row order");
   return gemm_packed(a, dtype, n_src, packed, K, kv, C, transpose, has_bias, pairs_perm, M,
                      nullptr, nullptr, plan, plan_bytes, out, out_dtype, as_stream(stream),
-                     row_order, thin_tiles != 0);
+                     row_order, thin_tiles != 0, row_words, int(words_per_row));
 }
 
 int sp_conv_fwd(const void* x, int32_t dtype, int64_t n_in, int64_t C, const void* w,

@@ -116,7 +116,7 @@ _SIGNATURES = {
     "sp_conv_gemm_planned": (ctypes.c_int, [_P, _I32, _I64, _P, _I64, _I64, _I64, _I32, _I32, _P,
                                             _I64, _P, _SZ, _P, _I32, _P]),
     "sp_conv_gemm_ordered": (ctypes.c_int, [_P, _I32, _I64, _P, _I64, _I64, _I64, _I32, _I32, _P,
-                                            _I64, _P, _P, _SZ, _I32, _P, _I32, _P]),
+                                            _I64, _P, _P, _SZ, _I32, _P, _I32, _P, _I32, _P]),
     "sp_permute_table": (ctypes.c_int, [_P, _I64, _I64, _P, _P, _P, _P]),
     "sp_table_stats": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _P]),
     "sp_conv_fwd": (ctypes.c_int, [_P, _I32, _I64, _I64, _P, _I32, _I64, _I64, _P, _I64, _P,

@@ -326,6 +326,7 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool 
     if sure or (done > 0 and natural[0] < ORDER_MAX_EFFICIENCY * done):
         order, words = mask_order(pairs, with_words=True)
         perm = permute_table(pairs, order, words if kv <= 32 else None)
+        perm._spconv_triton_words = words  # the unplanned kernel reads live offsets only
         masked = table_stats(perm, n_src) if not sure else None
         if sure or mfma_rows(masked) <= ORDER_MAX_WORK_RATIO * done:
             plan = gather_plan(perm, n_src) if planned else None
@@ -426,10 +427,12 @@ def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: 
     if variant is not None:
         order, perm, plan = variant
         thin = THIN_TILES if THIN_TILES != "auto" else getattr(perm, "_spconv_triton_thin", False)
+        words = getattr(perm, "_spconv_triton_words", None)  # sorted mask words [M, mic]
         _lib.check(L.sp_conv_gemm_ordered(
             _lib.ptr(a), _lib.dtype_code(a.dtype), a.shape[0], _lib.ptr(packed), K, kv, C,
             int(transpose), int(bias is not None), _lib.ptr(perm), M, _lib.ptr(order),
-            _lib.ptr(plan), 0 if plan is None else plan.numel(), int(bool(thin)), _lib.ptr(out),
+            _lib.ptr(plan), 0 if plan is None else plan.numel(), int(bool(thin)),
+            _lib.ptr(words), 0 if words is None else words.shape[1], _lib.ptr(out),
             _lib.dtype_code(out.dtype), _lib.stream_of(a.device)), "sp_conv_gemm_ordered")
         return
     if plan is not None:
