@@ -248,18 +248,33 @@ __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
 }
 
 // Single workgroup: ascending list of the overflow tiles and their number.
-__global__ __launch_bounds__(256) void plan_overflow_kernel(const int32_t* __restrict__ count,
-                                                            int64_t ntiles,
-                                                            int32_t* __restrict__ n_overflow,
-                                                            int32_t* __restrict__ overflow) {
-  __shared__ uint32_t scan_lds[256 / 64 + 1];
+// One workgroup; in each round thread i reads the counts of kOvPer consecutive
+// tiles at once (16 loads in flight instead of one round trip per 256 tiles),
+// so a round covers 16384 tiles; a block scan of the threads' overflow counts
+// places their tiles in ascending order.
+constexpr int kOvThreads = 1024;
+constexpr int kOvPer = 16;
+__global__ __launch_bounds__(kOvThreads) void plan_overflow_kernel(
+    const int32_t* __restrict__ count, int64_t ntiles, int32_t* __restrict__ n_overflow,
+    int32_t* __restrict__ overflow) {
+  __shared__ uint32_t scan_lds[kOvThreads / 64 + 1];
+  static_assert(kOvPer <= 32, "a thread's overflow flags are one 32-bit mask");
   uint32_t base = 0;
-  for (int64_t t0 = 0; t0 < ntiles; t0 += 256) {
-    const int64_t t = t0 + threadIdx.x;
-    const bool over = t < ntiles && count[t] >= kLdsRows;
+  for (int64_t t0 = 0; t0 < ntiles; t0 += int64_t(kOvThreads) * kOvPer) {
+    const int64_t my0 = t0 + int64_t(threadIdx.x) * kOvPer;
+    int32_t c[kOvPer];
+#pragma unroll
+    for (int j = 0; j < kOvPer; ++j) c[j] = my0 + j < ntiles ? count[my0 + j] : 0;
+    uint32_t bits = 0;
+#pragma unroll
+    for (int j = 0; j < kOvPer; ++j) bits |= (c[j] >= kLdsRows ? 1u : 0u) << j;
     uint32_t total;
-    const uint32_t pos = block_exclusive_scan<256>(over ? 1u : 0u, scan_lds, &total);
-    if (over) overflow[base + pos] = int32_t(t);
+    uint32_t pos = block_exclusive_scan<kOvThreads>(uint32_t(__popc(bits)), scan_lds, &total);
+    while (bits) {
+      const int j = __builtin_ctz(bits);
+      overflow[base + pos++] = int32_t(my0 + j);
+      bits &= bits - 1u;
+    }
     base += total;
   }
   if (threadIdx.x == 0) *n_overflow = int32_t(base);
@@ -403,7 +418,7 @@ int sp_gather_plan_build(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_
   else if (n_ent <= 8192) launch_plan<8192>(nt, s, pairs, M, k, n_src, p, b);
   else launch_plan<16384>(nt, s, pairs, M, k, n_src, p, b);
   SP_LAUNCHED();
-  plan_overflow_kernel<<<1, 256, 0, s>>>(count, p.ntiles, n_ovf, ovf);
+  plan_overflow_kernel<<<1, kOvThreads, 0, s>>>(count, p.ntiles, n_ovf, ovf);
   SP_LAUNCHED();
   if (n_overflow) {  // the count is only reported on request (it costs a sync)
     int32_t h = 0;

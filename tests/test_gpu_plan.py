@@ -156,6 +156,28 @@ def test_plan_matches_numpy(case):
         assert n_over == 0
 
 
+def test_plan_overflow_list_many_tiles():
+    """The overflow list of a table with more tiles than one round of the
+    listing kernel covers (17 000 tiles, 16 384 per round): every 7th tile
+    references 1 024 distinct sources (overflow), the others 64.  Counts and
+    the ascending overflow list against numpy."""
+    from spconv_triton.pytorch._impl import gemm
+
+    nt, kv = 17_000, 4
+    M = nt * TILE
+    col = np.arange(M)
+    tile, r = col // TILE, col % TILE
+    over = np.arange(nt) % 7 == 3
+    t = np.empty((kv, M), dtype=np.int32)
+    for k in range(kv):
+        t[k] = np.where(over[tile], tile * 1024 + k * TILE + r, tile * 1024 + r % 64)
+    plan = gemm.gather_plan(torch.from_numpy(t).to(DEV), nt * 1024)
+    P = _parse(plan, kv, M)
+    np.testing.assert_array_equal(P["count"], np.where(over, 1024, 64))
+    assert gemm.plan_overflow_count(plan) == P["n_ovf"] == int(over.sum())
+    np.testing.assert_array_equal(P["ovf"], np.nonzero(over)[0].astype(np.int32))
+
+
 def _both(a, w, bias, transpose, pairs, M, out_dtype=None):
     from spconv_triton.pytorch._impl import gemm
 
