@@ -15,7 +15,9 @@
 // tiles, the histograms are stored tile-major and every scatter workgroup
 // sums them itself (coalesced rows, 32 tiles per memory round trip, then a
 // block scan), so a pass is two launches; above that they are stored
-// digit-major and a device-wide exclusive scan gives the placements.  The
+// digit-major, one workgroup per digit scans its row over the tiles in place
+// and writes the digit's total, and every scatter workgroup scans the 512
+// totals itself: three launches.  The
 // first pass of a row sort generates the row indices itself.
 #include "sp_sort.h"
 
@@ -137,11 +139,43 @@ __device__ __forceinline__ void fused_tile_base(const uint32_t* __restrict__ his
   if (d < R) tile_base[d] = run + pre;
 }
 
+// Digit-major histograms [R][ntiles]: exclusive scan of digit blockIdx.x's
+// row over the tiles, in place, and the digit's total.
+constexpr int kDsThreads = 256;
+constexpr int kDsPer = 8;  // consecutive tiles per thread and round
+__global__ __launch_bounds__(kDsThreads) void rs_digit_prefix(uint32_t* __restrict__ hist,
+                                                             int64_t ntiles,
+                                                             uint32_t* __restrict__ totals) {
+  __shared__ uint32_t scan_lds[kDsThreads / 64 + 1];
+  uint32_t* row = hist + int64_t(blockIdx.x) * ntiles;
+  uint32_t base = 0;
+  for (int64_t t0 = 0; t0 < ntiles; t0 += int64_t(kDsThreads) * kDsPer) {
+    const int64_t my0 = t0 + int64_t(threadIdx.x) * kDsPer;
+    uint32_t v[kDsPer];
+    uint32_t sum = 0;
+#pragma unroll
+    for (int j = 0; j < kDsPer; ++j) {
+      v[j] = my0 + j < ntiles ? row[my0 + j] : 0u;
+      sum += v[j];
+    }
+    uint32_t tot;
+    uint32_t run = base + block_exclusive_scan<kDsThreads>(sum, scan_lds, &tot);
+#pragma unroll
+    for (int j = 0; j < kDsPer; ++j) {
+      if (my0 + j < ntiles) row[my0 + j] = run;
+      run += v[j];
+    }
+    base += tot;
+  }
+  if (threadIdx.x == 0) totals[blockIdx.x] = base;
+}
+
 template <class Item, class Digit>
 __global__ __launch_bounds__(kRsThreads) void rs_scatter(const Item* __restrict__ in,
                                                         Item* __restrict__ out, int64_t n,
                                                         Digit dig, int db,
                                                         const uint32_t* __restrict__ offsets,
+                                                        const uint32_t* __restrict__ totals,
                                                         int64_t ntiles) {
   __shared__ __align__(16) uint16_t seg[kRsSegs][kRsMaxRadix];
   __shared__ uint32_t tile_base[kRsMaxRadix];
@@ -171,8 +205,14 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter(const Item* __restrict_
     // the segment counts below)
     fused_tile_base(offsets, ntiles, R, tile_base, scan_lds);
   } else {
-    for (int i = threadIdx.x; i < R; i += kRsThreads)
-      tile_base[i] = offsets[int64_t(i) * ntiles + blockIdx.x];
+    // digit d's items start after all items of smaller digits (a block scan of
+    // the totals; thread d owns digit d) and after its items in earlier tiles
+    const int d = int(threadIdx.x);
+    const uint32_t t = d < R ? totals[d] : 0u;
+    const uint32_t pre = d < R ? offsets[int64_t(d) * ntiles + blockIdx.x] : 0u;
+    uint32_t all = 0;
+    const uint32_t below = block_exclusive_scan<kRsThreads>(t, scan_lds, &all);
+    if (d < R) tile_base[d] = below + pre;
     __syncthreads();
   }
 #pragma unroll
@@ -215,7 +255,7 @@ __global__ __launch_bounds__(kRsThreads) void rs_scatter(const Item* __restrict_
 
 struct RsBuffers {
   uint32_t* hist;
-  void* scan_ws;
+  uint32_t* totals;  // kRsMaxRadix digit totals (digit-major histograms)
 };
 
 static size_t rs_hist_words(int64_t n) {
@@ -233,12 +273,11 @@ static int radix_pass(const Item* in, Item* out, int64_t n, Digit dig, int db, c
                                                                           b.hist, ntiles);
   SP_LAUNCHED();
   if (ntiles > kRsFusedTiles) {
-    int rc = exclusive_scan_u32(b.hist, b.hist, (int64_t(1) << db) * ntiles, nullptr, b.scan_ws,
-                                s);
-    if (rc) return rc;
+    rs_digit_prefix<<<dim3(1u << db), dim3(kDsThreads), 0, s>>>(b.hist, ntiles, b.totals);
+    SP_LAUNCHED();
   }
-  rs_scatter<Item, Digit><<<dim3(unsigned(ntiles)), dim3(kRsThreads), 0, s>>>(in, out, n, dig, db,
-                                                                             b.hist, ntiles);
+  rs_scatter<Item, Digit><<<dim3(unsigned(ntiles)), dim3(kRsThreads), 0, s>>>(
+      in, out, n, dig, db, b.hist, b.totals, ntiles);
   SP_LAUNCHED();
   return SP_OK;
 }
@@ -257,7 +296,7 @@ static void rows_layout(W& w, int64_t n) {
   w.template take<uint32_t>(size_t(n));                  // perm A
   w.template take<uint32_t>(size_t(n));                  // perm B
   w.template take<uint32_t>(rs_hist_words(n));           // histograms
-  w.template take<char>(scan_workspace_bytes(int64_t(rs_hist_words(n))));
+  w.template take<uint32_t>(size_t(kRsMaxRadix));         // digit totals
 }
 
 size_t sort_rows_ws_bytes(int64_t n) {
@@ -278,7 +317,7 @@ int sort_rows_by_words(const uint32_t* words, int64_t n, int mic, int kv, uint32
   uint32_t* b = c.take<uint32_t>(size_t(n));
   RsBuffers bufs;
   bufs.hist = c.take<uint32_t>(rs_hist_words(n));
-  bufs.scan_ws = c.take<char>(scan_workspace_bytes(int64_t(rs_hist_words(n))));
+  bufs.totals = c.take<uint32_t>(size_t(kRsMaxRadix));
   bool first = true;  // the first pass reads the identity permutation implicitly
   for (int w = 0; w < mic; ++w) {
     int bits = (w < mic - 1) ? 32 : kv - 32 * (mic - 1);
@@ -314,7 +353,7 @@ int sort_rows_by_words(const uint32_t* words, int64_t n, int mic, int kv, uint32
 template <class W>
 static void keys_layout(W& w, int64_t n) {
   w.template take<uint32_t>(rs_hist_words(n));
-  w.template take<char>(scan_workspace_bytes(int64_t(rs_hist_words(n))));
+  w.template take<uint32_t>(size_t(kRsMaxRadix));  // digit totals
 }
 
 size_t sort_keys_ws_bytes(int64_t n) {
@@ -329,7 +368,7 @@ static int sort_keys_impl(Item* keys, Item* tmp, int64_t n, int bits, Item** res
   WsCursor c(ws, ~size_t(0));
   RsBuffers bufs;
   bufs.hist = c.take<uint32_t>(rs_hist_words(n));
-  bufs.scan_ws = c.take<char>(scan_workspace_bytes(int64_t(rs_hist_words(n))));
+  bufs.totals = c.take<uint32_t>(size_t(kRsMaxRadix));
   Item* a = keys;
   Item* b = tmp;
   int widths[8];
