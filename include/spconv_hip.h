@@ -223,9 +223,13 @@ int sp_conv_gemm_packed(const void* a, int32_t dtype, int64_t n_src, const void*
  * sp_conv_gemm_packed).  sp_gather_plan_build is asynchronous; n_overflow
  * (nullable) requests the number of tiles whose distinct rows do not fit in
  * LDS (the GEMM gathers those directly from memory), which costs one stream
- * synchronization. */
+ * synchronization.  row_words (nullable): the rows' mask words, words_per_row
+ * (>= ceil(kv / 32)) per row (bit k of row r set iff pairs[k, r] >= 0); the
+ * builder then reads only the entries of the offsets some row of a tile has
+ * (the same plan, built faster for tables with few pairs per row). */
 size_t sp_gather_plan_bytes(int64_t M, int64_t kv);
-int sp_gather_plan_build(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_src, void* plan,
+int sp_gather_plan_build(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_src,
+                         const uint32_t* row_words, int32_t words_per_row, void* plan,
                          size_t plan_bytes, int64_t* n_overflow, void* stream);
 
 /* sp_conv_gemm_packed with a gather plan of `pairs` (built for the same kv, M

@@ -30,7 +30,8 @@ template <int NP>
 __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
     const int32_t* __restrict__ pairs, int64_t M, int kv, int64_t n_src,
     int32_t* __restrict__ count, int32_t* __restrict__ rows_out, int32_t* __restrict__ nact_out,
-    int32_t* __restrict__ koff_out, uint16_t* __restrict__ addr_out, int E) {
+    int32_t* __restrict__ koff_out, uint16_t* __restrict__ addr_out, int E,
+    const uint32_t* __restrict__ words, int mic) {
   // sort path: the entries; bitmap path: NP / 2 bitmap words, then NP / 2
   // word rank offsets
   __shared__ int32_t keys[NP];
@@ -47,8 +48,22 @@ __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
   const int64_t r0 = tile * kTileRows;
   const int n_ent = kTileRows * kv;
 
+  // with the rows' mask words, the offsets no row of the tile has are not read
+  __shared__ uint32_t s_live[2];
   if (tid < kPlanMaxKv) s_item[tid] = -1;
+  if (tid < 2) s_live[tid] = words ? 0u : 0xffffffffu;
   __syncthreads();
+  if (words) {  // (uniform)
+    const int64_t r = r0 + tid;
+    if (tid < kTileRows && r < M) {
+      const uint32_t* wr = words + r * int64_t(mic);
+      const uint32_t w0 = wr[0], w1 = mic > 1 ? wr[1] : 0u;
+      if (w0) atomicOr(&s_live[0], w0);
+      if (w1) atomicOr(&s_live[1], w1);
+    }
+    __syncthreads();
+  }
+  const uint64_t live = (uint64_t(s_live[1]) << 32) | s_live[0];
   // ---- entries into registers; window and items
   int32_t v[PER];
   int32_t lo = kNone, hi = -1;
@@ -59,7 +74,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
     if (e < n_ent) {
       const int k = e / kTileRows;
       const int64_t r = r0 + (e - k * kTileRows);
-      if (r < M) {
+      if (r < M && ((live >> k) & 1u)) {
         const int32_t x = pairs[int64_t(k) * M + r];
         if (x >= 0 && x < n_src) {
           key = x;
@@ -372,12 +387,13 @@ __global__ __launch_bounds__(256) void permute_table_kernel(const int32_t* __res
 
 template <int NP>
 static void launch_plan(unsigned nt, hipStream_t s, const int32_t* pairs, int64_t M, int kv,
-                        int64_t n_src, const PlanLayout& p, char* b) {
+                        int64_t n_src, const PlanLayout& p, char* b, const uint32_t* words,
+                        int mic) {
   plan_build_kernel<NP><<<nt, kPlanThreads, 0, s>>>(
       pairs, M, kv, n_src, reinterpret_cast<int32_t*>(b + p.count_off),
       reinterpret_cast<int32_t*>(b + p.rows_off), reinterpret_cast<int32_t*>(b + p.nact_off),
       reinterpret_cast<int32_t*>(b + p.koff_off), reinterpret_cast<uint16_t*>(b + p.addr_off),
-      p.E);
+      p.E, words, mic);
 }
 
 }  // namespace sp
@@ -391,10 +407,13 @@ size_t sp_gather_plan_bytes(int64_t M, int64_t kv) {
   return plan_layout(M, kv).total;
 }
 
-int sp_gather_plan_build(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_src, void* plan,
+int sp_gather_plan_build(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_src,
+                         const uint32_t* row_words, int32_t words_per_row, void* plan,
                          size_t plan_bytes, int64_t* n_overflow, void* stream) {
   SP_CHECK_ARG(kv >= 1 && kv <= kPlanMaxKv, "gather plan: kv=%lld outside 1..%d", (long long)kv,
                kPlanMaxKv);
+  SP_CHECK_ARG(!row_words || (words_per_row >= (kv + 31) / 32 && words_per_row <= 1024),
+               "gather plan: %d mask words per row for kv=%lld", words_per_row, (long long)kv);
   SP_CHECK_ARG(M >= 0 && M < (int64_t(1) << 31) && n_src >= 0 && n_src < (int64_t(1) << 31),
                "gather plan: bad sizes M=%lld n_src=%lld", (long long)M, (long long)n_src);
   if (n_overflow) *n_overflow = 0;
@@ -412,11 +431,11 @@ int sp_gather_plan_build(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_
   const unsigned nt = unsigned(p.ntiles);
   const int n_ent = kTileRows * int(kv);
   const int k = int(kv);
-  if (n_ent <= 1024) launch_plan<1024>(nt, s, pairs, M, k, n_src, p, b);
-  else if (n_ent <= 2048) launch_plan<2048>(nt, s, pairs, M, k, n_src, p, b);
-  else if (n_ent <= 4096) launch_plan<4096>(nt, s, pairs, M, k, n_src, p, b);
-  else if (n_ent <= 8192) launch_plan<8192>(nt, s, pairs, M, k, n_src, p, b);
-  else launch_plan<16384>(nt, s, pairs, M, k, n_src, p, b);
+  if (n_ent <= 1024) launch_plan<1024>(nt, s, pairs, M, k, n_src, p, b, row_words, words_per_row);
+  else if (n_ent <= 2048) launch_plan<2048>(nt, s, pairs, M, k, n_src, p, b, row_words, words_per_row);
+  else if (n_ent <= 4096) launch_plan<4096>(nt, s, pairs, M, k, n_src, p, b, row_words, words_per_row);
+  else if (n_ent <= 8192) launch_plan<8192>(nt, s, pairs, M, k, n_src, p, b, row_words, words_per_row);
+  else launch_plan<16384>(nt, s, pairs, M, k, n_src, p, b, row_words, words_per_row);
   SP_LAUNCHED();
   plan_overflow_kernel<<<1, kOvThreads, 0, s>>>(count, p.ntiles, n_ovf, ovf);
   SP_LAUNCHED();

@@ -145,13 +145,15 @@ def _use_plan(M: int, C: int, K: int) -> bool:
     return bool(USE_GATHER_PLAN)
 
 
-def gather_plan(pairs: torch.Tensor, n_src: int):
+def gather_plan(pairs: torch.Tensor, n_src: int, words: torch.Tensor | None = None):
     """Gather plan of a [kv, M] pair table (``sp_gather_plan_build``), or None
     when kv is outside the planned kernel's range.  Memoised on the table
     tensor, like the reference memoises its tables on the indice data
     (pairs.py:429-469); rebuilt if the table is modified in place.  The build
     is asynchronous (no host synchronization).  None as well while the stream
-    is being captured and no plan is cached (the GEMM then gathers directly)."""
+    is being captured and no plan is cached (the GEMM then gathers directly).
+    words: the rows' mask words [M, mic] (nullable), which let the build skip
+    the entries of offsets a tile's rows do not have (the same plan)."""
     kv, M = pairs.shape
     cached = getattr(pairs, "_spconv_triton_plan", None)
     stamp = (int(n_src), pairs._version, pairs.data_ptr())
@@ -164,8 +166,9 @@ def gather_plan(pairs: torch.Tensor, n_src: int):
     if nbytes == 0:
         return None
     plan = torch.empty(nbytes, dtype=torch.uint8, device=pairs.device)
-    _lib.check(L.sp_gather_plan_build(_lib.ptr(pairs), kv, M, int(n_src), _lib.ptr(plan), nbytes,
-                                      None, _lib.stream_of(pairs.device)),
+    _lib.check(L.sp_gather_plan_build(_lib.ptr(pairs), kv, M, int(n_src), _lib.ptr(words),
+                                      0 if words is None else words.shape[1], _lib.ptr(plan),
+                                      nbytes, None, _lib.stream_of(pairs.device)),
                "sp_gather_plan_build")
     pairs._spconv_triton_plan = (stamp, plan)
     return plan
@@ -302,7 +305,8 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool 
         if not (plan_ok and kv <= _PLAN_MAX_KV):
             return step if plan is None else (order, perm, None)
         if plan is None and not torch.cuda.is_current_stream_capturing():
-            step = (order, perm, gather_plan(perm, n_src))
+            step = (order, perm, gather_plan(perm, n_src, getattr(perm, "_spconv_triton_words",
+                                                                   None)))
             pairs._spconv_triton_order = (stamp, step)
         return step
     if step == "natural" or (mode == "auto" and (work < ORDER_MIN_WORK or kv > _STATS_MAX_KV)):
@@ -329,7 +333,7 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool 
         perm._spconv_triton_words = words  # the unplanned kernel reads live offsets only
         masked = table_stats(perm, n_src) if not sure else None
         if sure or mfma_rows(masked) <= ORDER_MAX_WORK_RATIO * done:
-            plan = gather_plan(perm, n_src) if planned else None
+            plan = gather_plan(perm, n_src, words) if planned else None
             variant = (order, perm, plan)
             tiles = (M + 255) // 256
             perm._spconv_triton_thin = (

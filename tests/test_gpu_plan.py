@@ -156,6 +156,35 @@ def test_plan_matches_numpy(case):
         assert n_over == 0
 
 
+@pytest.mark.parametrize("kv", [27, 64])
+def test_plan_with_row_words_identical(kv):
+    """A plan built with the rows' mask words (the build reads only the offsets
+    some row of a tile has) equals the plan built from the table alone in
+    every part the GEMM reads (counts, overflow list, distinct rows, items and
+    their addresses up to the tile's last group), on a mask-ordered sparse
+    table (few live offsets per tile) and a denser one."""
+    from spconv_triton.pytorch._impl import gemm
+
+    rng = np.random.default_rng(21)
+    M = 5000
+    for p_valid in (0.03, 0.5):
+        pf = _random_table(rng, kv, M, 20_000, p_valid).contiguous()
+        order, words = gemm.mask_order(pf, with_words=True)
+        perm = gemm.permute_table(pf, order, words if kv <= 32 else None)
+        A = _parse(gemm.gather_plan(perm.clone(), 20_000), kv, M)
+        B = _parse(gemm.gather_plan(perm, 20_000, words), kv, M)
+        for key in ("count", "ovf", "nact"):
+            np.testing.assert_array_equal(A[key], B[key], f"{key}, p_valid={p_valid}")
+        for t in range(A["count"].shape[0]):
+            if A["count"][t] >= LDS_ROWS:
+                continue
+            n = int(A["nact"][t])
+            n4 = (n + GROUP - 1) // GROUP * GROUP
+            np.testing.assert_array_equal(A["rows"][t], B["rows"][t])
+            np.testing.assert_array_equal(A["koff"][t], B["koff"][t])
+            np.testing.assert_array_equal(A["addr"][t, :n4], B["addr"][t, :n4])
+
+
 def test_plan_overflow_list_many_tiles():
     """The overflow list of a table with more tiles than one round of the
     listing kernel covers (17 000 tiles, 16 384 per round): every 7th tile
