@@ -264,9 +264,9 @@ __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
 
 // Single workgroup: ascending list of the overflow tiles and their number.
 // One workgroup; in each round thread i reads the counts of kOvPer consecutive
-// tiles at once (16 loads in flight instead of one round trip per 256 tiles),
-// so a round covers 16384 tiles; a block scan of the threads' overflow counts
-// places their tiles in ascending order.
+// tiles at once (16 loads in flight), so one memory round trip covers 16384
+// tiles; a block scan of the threads' overflow counts places their tiles in
+// ascending order.
 constexpr int kOvThreads = 1024;
 constexpr int kOvPer = 16;
 __global__ __launch_bounds__(kOvThreads) void plan_overflow_kernel(
