@@ -504,8 +504,9 @@ def test_mask_row_order_full_size(case):
     """The stress configurations at their stated sizes: SubMConv3d 256 -> 256 on
     a 400k-voxel 1024^3 surface cloud (staged kernel, overflow tiles in mask
     order) and SubMConv4d 3^4 128 -> 128 at ~500k voxels (kv = 81: direct
-    kernel).  The mask-ordered forward equals the natural one bit for bit, and
-    the automatic rule picks the mask order for both."""
+    kernel).  The mask-ordered forward equals the natural one bit for bit, the
+    rulebook and every 40th output row match the oracle, and the automatic
+    rule picks the mask order for both."""
     from bench_data import surface_cloud
     from spconv_triton.core import ConvAlgo
     from spconv_triton.pytorch import ops
@@ -546,23 +547,24 @@ def test_mask_row_order_full_size(case):
     order = gemm.mask_order(pf)
     assert torch.equal(torch.sort(order.long())[0], torch.arange(n, device=DEV)), \
         "the mask order must be a permutation of the rows"
-    if case == "subm4d":
-        # config 5 case 1 against the oracle at its stated size: the 4-D int64
-        # rulebook bit for bit, and every 40th output row of the GEMM
-        from spconv_triton.pytorch._impl import pairs as P
+    # both configurations against the oracle at their stated sizes: the
+    # rulebook (pair table, sorted masks and argsort) bit for bit -- int64
+    # keys for the 4-D grid -- and every 40th output row of the GEMM
+    from spconv_triton.pytorch._impl import pairs as P
 
-        assert P.key_is_int64(1, shape, shape, True)
-        exp = orc.igemm_pairs(idx, 1, shape, ks, [1] * nd, [1] * nd, [1] * nd, [0] * nd, True,
-                              False, False)
-        np.testing.assert_array_equal(pf.cpu().numpy(), exp[2])
-        np.testing.assert_array_equal(res[4][0].cpu().numpy(), exp[4][0])
-        np.testing.assert_array_equal(res[6][0].cpu().numpy(), exp[6][0])
-        rows = torch.arange(0, n, 40, device=DEV)
-        ref = orc.gemm_fwd(x.double().cpu().numpy(), w.double().cpu().numpy(),
-                           pf[:, rows].cpu().numpy())
-        out = outs["natural"][rows].double().cpu().numpy()
+    assert P.key_is_int64(1, shape, shape, True) == (case == "subm4d")
+    exp = orc.igemm_pairs(idx, 1, shape, ks, [1] * nd, [1] * nd, [1] * nd, [0] * nd, True,
+                          False, False)
+    np.testing.assert_array_equal(pf.cpu().numpy(), exp[2])
+    np.testing.assert_array_equal(res[4][0].cpu().numpy(), exp[4][0])
+    np.testing.assert_array_equal(res[6][0].cpu().numpy(), exp[6][0])
+    rows = torch.arange(0, n, 40, device=DEV)
+    ref = orc.gemm_fwd(x.double().cpu().numpy(), w.double().cpu().numpy(),
+                       pf[:, rows].cpu().numpy())
+    for mode in ("natural", "mask"):
+        out = outs[mode][rows].double().cpu().numpy()
         bad = np.abs(out - ref) > 1e-3 * np.abs(ref) + 1e-5
-        assert not bad.any(), f"{int(bad.sum())} of {bad.size} beyond the fp16 bound"
+        assert not bad.any(), f"{mode}: {int(bad.sum())} of {bad.size} beyond the fp16 bound"
     pf2 = pf.clone()  # a fresh table: the automatic rule decides at its second wide call
     assert gemm.row_order_variant(pf2, n, C * C) is None
     assert gemm.row_order_variant(pf2, n, C * C) is not None

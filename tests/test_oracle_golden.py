@@ -289,6 +289,32 @@ def test_oracle_gemm_against_dense_conv():
     assert abs(lhs - float((dW * W.reshape(K, 27, C)).sum())) < 1e-9 * max(1.0, abs(lhs))
 
 
+def test_oracle_gemm_fwd_f32_matches_fp64():
+    """The fp32 gather-GEMM (timed as bench.py's CPU baseline) against the fp64
+    one pinned above: same pairs, bias and layout, within fp32 accumulation
+    error, |out32 - out64| <= 1e-5 * S + 1e-6 with S = sum |x||w| (the fp64
+    GEMM of |X| and |W|).  A dropped offset, a transposed weight or a missing
+    bias moves entries by O(S) and fails the bound; the random table has empty
+    entries (-1) and rows without any pair."""
+    rng = np.random.default_rng(12)
+    n_in, n_out, C, K, kv = 700, 500, 24, 40, 27
+    pf = rng.integers(0, n_in, size=(kv, n_out)).astype(np.int32)
+    pf[rng.random((kv, n_out)) > 0.35] = -1
+    pf[:, 17] = -1  # a row without any pair: bias only
+    X = rng.standard_normal((n_in, C)).astype(np.float32)
+    W = rng.standard_normal((K, kv, C)).astype(np.float32)
+    b = rng.standard_normal(K).astype(np.float32)
+    ref = orc.gemm_fwd(X, W, pf, b)
+    out = orc.gemm_fwd_f32(X, W, pf, b)
+    assert out.dtype == np.float32 and out.shape == (n_out, K)
+    S = orc.gemm_fwd(np.abs(X), np.abs(W), pf)
+    err = np.abs(out.astype(np.float64) - ref)
+    assert (err <= 1e-5 * S + 1e-6).all(), f"max err/S {(err / np.maximum(S, 1e-30)).max():.2e}"
+    np.testing.assert_array_equal(out[17], b)
+    no_bias = orc.gemm_fwd_f32(X, W, pf)
+    np.testing.assert_array_equal(no_bias[17], np.zeros(K, np.float32))
+
+
 def _canon_voxels(idx, vox, npv):
     """Voxels sorted by coordinate, points inside a voxel sorted
     lexicographically (the reference's canonical form, tests/helpers.py:442-465)."""
