@@ -1,3 +1,8 @@
+# SPDX-FileCopyrightText: Copyright contributors to the spconv-Triton project
+# SPDX-FileCopyrightText: Derived from spconv, Copyright 2021 Yan Yan and contributors
+# SPDX-License-Identifier: Apache-2.0
+# The public names, signatures and error messages in this file follow spconv-Triton's
+# API (Apache-2.0); the implementation is this package's own.
 """Public PyTorch API, a drop-in for ``spconv.pytorch`` / ``spconv_triton.pytorch``."""
 
 from spconv_triton.pytorch import functional, ops
