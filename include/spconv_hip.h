@@ -73,6 +73,13 @@ typedef struct sp_geom {
 } sp_geom;
 
 /* ---- library info ------------------------------------------------------ */
+/* Revision of the argument lists declared here.  It changes whenever an
+ * entry point's arguments change (revision 2: sp_pairgen_conv_build,
+ * sp_gather_plan_build, sp_conv_gemm_ordered and sp_permute_table took their
+ * current forms).  A caller compares sp_abi_version() with the value it was
+ * compiled against and must not call into a library of another revision. */
+#define SP_ABI_VERSION 2
+int sp_abi_version(void);
 int sp_version(void);              /* (major << 16) | (minor << 8) | patch */
 const char* sp_arch(void);         /* offload target the code objects hold */
 const char* sp_last_error(void);   /* message of the last failing call (thread-local) */

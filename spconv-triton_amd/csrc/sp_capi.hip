@@ -154,6 +154,8 @@ int exclusive_scan_popc(const uint32_t* words, uint32_t* out, int64_t len, uint3
 
 extern "C" {
 
+int sp_abi_version(void) { return SP_ABI_VERSION; }
+
 int sp_version(void) { return (0 << 16) | (1 << 8) | 0; }
 
 const char* sp_arch(void) { return "gfx950"; }

@@ -561,17 +561,21 @@ static void conv_layout(W& w, const GeomDev& g, int64_t n, bool key64, ConvWs* o
 // The bitmap's passes cost in proportion to the output volume, the hash
 // path's in proportion to the candidates (n * kv, each an insert with probing,
 // then a radix sort and a ranking pass): the bitmap is taken up to 4096 cells
-// per input row or 1024 per candidate.  (Measured on a transposed k3 s2 conv
-// of 50k uniform voxels in 41 x 1600 x 1408: 749M output cells, 15k per row
-// but 555 per candidate; the hash path's insert alone took 270 us.)
+// per input row, or 1024 per candidate while the bitmap and its prefix stay
+// within kBitmapMaxCandidateCells cells (256 MiB of workspace; the hash
+// path's is O(n * kv)).  (Measured on a transposed k3 s2 conv of 50k uniform
+// voxels in 41 x 1600 x 1408: 749M output cells, 15k per row but 555 per
+// candidate; the hash path's insert alone took 270 us.)
 constexpr int64_t kBitmapCellsPerRow = 4096;
 constexpr int64_t kBitmapCellsPerCandidate = 1024;
+constexpr double kBitmapMaxCandidateCells = double(int64_t(1) << 30);
 
 static bool conv_bitmap(const GeomDev& g, int64_t n, bool key64) {
   if (key64) return false;
   const double vol = double(g.batch) * double(prod_shape(g.out_shape, g.ndim));
   return vol <= double(kBitmapCellsPerRow) * double(n) ||
-         vol <= double(kBitmapCellsPerCandidate) * double(n) * double(g.kv);
+         (vol <= kBitmapMaxCandidateCells &&
+          vol <= double(kBitmapCellsPerCandidate) * double(n) * double(g.kv));
 }
 
 struct BitmapWs {

@@ -596,6 +596,9 @@ extern "C" {
 
 int sp_sort_dropped_positions(uint64_t* count, int32_t reset) {
   SP_CHECK_ARG(count, "sort drops: null pointer");
+  // sorts may still run on any stream of the current device (torch's side
+  // streams do not synchronise with the null stream): wait for all of them
+  SP_HIP(hipDeviceSynchronize());
   unsigned long long v = 0;
   SP_HIP(hipMemcpyFromSymbol(&v, HIP_SYMBOL(g_sort_drops), sizeof(v)));
   *count = uint64_t(v);

@@ -86,6 +86,7 @@ _GP = ctypes.POINTER(Geom)
 
 # name -> (restype, argtypes); must match include/spconv_hip.h
 _SIGNATURES = {
+    "sp_abi_version": (ctypes.c_int, []),
     "sp_version": (ctypes.c_int, []),
     "sp_arch": (ctypes.c_char_p, []),
     "sp_last_error": (ctypes.c_char_p, []),
@@ -150,6 +151,9 @@ _SIGNATURES = {
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)
 
+#: SP_ABI_VERSION of include/spconv_hip.h that _SIGNATURES follows.
+ABI_VERSION = 2
+
 
 def _hip_runtimes_mapped() -> set[str]:
     try:
@@ -180,6 +184,11 @@ def load_library(path: str | None = None) -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    if lib.sp_abi_version() != ABI_VERSION:
+        raise RuntimeError(
+            f"{p} has C ABI revision {lib.sp_abi_version()}, these bindings expect "
+            f"{ABI_VERSION} (SP_ABI_VERSION of include/spconv_hip.h): rebuild the library"
+        )
     runtimes = _hip_runtimes_mapped()
     if len(runtimes) > 1:
         raise RuntimeError(

@@ -124,8 +124,13 @@ class _Tables:
 #: Dense cell -> row grids kept between subm builds, one per (device, stream):
 #: (grid, epoch of its last build).  A grid is zero-filled when created and
 #: every 255 builds; in between, each build stamps its cells with a new epoch
-#: (``sp_pairgen_subm_grid``), so no build clears it.
+#: (``sp_pairgen_subm_grid``), so no build clears it.  Only grids of at most
+#: KEEP_GRID_MAX_CELLS int32 cells are kept (a 256^3 volume plus its guard
+#: cells, 64 MiB); a build needing a larger one takes a per-build workspace,
+#: which the caching allocator can release.  ``release_pairgen_grids()`` drops
+#: the kept grids (a grid kept for a stream no longer in use stays until then).
 _GRIDS: dict = {}
+KEEP_GRID_MAX_CELLS = (1 << 24) + 1024
 
 
 def _subm_grid(device: torch.device, cells: int):
@@ -177,7 +182,8 @@ def _generate(indices, batch_size, spatial_shape, ksize, stride, padding, dilati
         pb = torch.empty((kv, N), **i32) if want_bwd else None
         words = torch.empty((N, mic), **i32) if want_words_fwd else None
         cells = L.sp_pairgen_subm_grid_cells(g, N)
-        if cells > 0 and not torch.cuda.is_current_stream_capturing():
+        if (0 < cells <= KEEP_GRID_MAX_CELLS
+                and not torch.cuda.is_current_stream_capturing()):
             # a grid kept between builds (a graph replays its kernels with the
             # epoch it was captured with, so captured builds clear their own)
             grid, epoch = _subm_grid(device, cells)

@@ -47,6 +47,9 @@ def test_library_identity_queries():
     L = _lib.load_library()
     assert L.sp_arch() == b"gfx950"
     assert L.sp_version() == (0 << 16) | (1 << 8)
+    header = (ROOT / "include" / "spconv_hip.h").read_text()
+    m = re.search(r"#define SP_ABI_VERSION (\d+)", header)
+    assert m and L.sp_abi_version() == int(m.group(1)) == _lib.ABI_VERSION
 
 
 def _geom(mode, shape, out_shape, ks=3, st=1, pad=1, dil=1, batch=1):

@@ -3,7 +3,9 @@ per-GPU scratch array instead of a caller workspace.  Called through the C
 ABI and compared bit for bit with sp_conv_fwd (same kernels, same summation
 order) on two calls in a row, the second on a smaller input, in each compute
 dtype; sizes above SP_NOALLOC_SCRATCH_BYTES are rejected with
-SP_ERR_UNSUPPORTED before any work is enqueued.
+SP_ERR_UNSUPPORTED before any work is enqueued; and the call allocates
+nothing (free device memory unchanged across calls, replays of a captured
+graph equal to the workspace forward).
 """
 
 import re
@@ -95,3 +97,57 @@ def test_noalloc_rejects_weights_beyond_scratch():
                                _lib.stream_of(dummy.device))
     assert rc == _lib.SP_ERR_UNSUPPORTED
     assert b"scratch" in L.sp_last_error()
+
+
+def test_noalloc_allocates_nothing():
+    """The entry point's contract: after the first call on the device (which
+    looks up the scratch array's address), calls of other sizes leave the
+    device's free memory unchanged, and the call can be captured into a HIP
+    graph whose replays -- with eager work and synchronisations between them
+    -- equal the workspace forward each time."""
+    from spconv_triton.pytorch._impl import _lib
+
+    L = _lib.lib()
+    dt = _lib.dtype_code(torch.float16)
+    cases = []
+    for i, (n, grid, C, K) in enumerate(((9000, 36, 64, 64), (2500, 20, 16, 32))):
+        pf, _, _ = _rulebook(n, grid, seed=30 + i)
+        torch.manual_seed(20 + i)
+        x = torch.randn(n, C, device=DEV).half()
+        w = (torch.randn(K, 27, C, device=DEV) / np.sqrt(27 * C)).half()
+        b = torch.randn(K, device=DEV).half()
+        out = torch.empty((n, K), dtype=torch.float16, device=DEV)
+        cases.append((x, w, b, pf, out))
+
+    def call(x, w, b, pf, out):
+        K, kv, C = w.shape
+        _lib.check(L.sp_conv_fwd_noalloc(_lib.ptr(x), dt, x.shape[0], C, _lib.ptr(w), dt, K, kv,
+                                         _lib.ptr(pf), pf.shape[1], _lib.ptr(b), None, None,
+                                         _lib.ptr(out), dt, _lib.stream_of(x.device)),
+                   "sp_conv_fwd_noalloc")
+
+    call(*cases[0])  # warm-up: scratch address lookup
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info(0)[0]
+    for c in (cases[1], cases[0], cases[1]):
+        call(*c)
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info(0)[0] == free0, "the no-allocation forward allocated memory"
+
+    x, w, b, pf, out = cases[1]
+    ref, _ = _both(x, w, b, pf, False, None, None, torch.float16)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            call(x, w, b, pf, out)
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(3):
+        out.fill_(float("nan"))
+        call(*cases[0])  # eager use of the shared scratch between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"graph replay {rep} differs from the workspace forward"
