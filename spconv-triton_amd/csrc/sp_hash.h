@@ -63,6 +63,21 @@ struct Table32 {
     return false;
   }
 
+  // The slot holding `key64`, inserting it (with value 0) when absent; -1
+  // (and the overflow flag) when the table is full.
+  __device__ int64_t insert_slot(uint64_t key64) const {
+    const uint32_t key = uint32_t(key64);
+    uint64_t s = home(key64);
+    for (uint64_t i = 0; i <= mask; ++i) {
+      const uint64_t prev = atomicCAS((unsigned long long*)&slots[s], (unsigned long long)kEmpty64,
+                                      (unsigned long long)key);
+      if (prev == kEmpty64 || uint32_t(prev) == key) return int64_t(s);
+      s = (s + 1) & mask;
+    }
+    atomicExch(overflow, 1);
+    return -1;
+  }
+
   __device__ __forceinline__ int64_t find_slot(uint64_t key64) const {
     const uint32_t key = uint32_t(key64);
     uint64_t s = home(key64);
@@ -71,6 +86,20 @@ struct Table32 {
       if (uint32_t(v) == key) return int64_t(s);
       if (v == kEmpty64) return -1;
       s = (s + 1) & mask;
+    }
+    return -1;
+  }
+
+  // Split lookups: load the home slot's word (several lookups can have theirs
+  // in flight at once), then finish from it.
+  __device__ __forceinline__ uint64_t word(uint64_t s) const { return slots[s]; }
+  __device__ __forceinline__ int64_t find_from(uint64_t s, uint64_t w, uint64_t key64) const {
+    const uint32_t key = uint32_t(key64);
+    for (uint64_t i = 0; i <= mask; ++i) {
+      if (uint32_t(w) == key) return int64_t(s);
+      if (w == kEmpty64) return -1;
+      s = (s + 1) & mask;
+      w = slots[s];
     }
     return -1;
   }
@@ -116,6 +145,20 @@ struct Table64 {
     return false;
   }
 
+  // The slot holding `key`, inserting it when absent (its value is left as
+  // is); -1 (and the overflow flag) when the table is full.
+  __device__ int64_t insert_slot(uint64_t key) const {
+    uint64_t s = home(key);
+    for (uint64_t i = 0; i <= mask; ++i) {
+      const uint64_t prev = atomicCAS((unsigned long long*)&keys[s], (unsigned long long)kEmpty64,
+                                      (unsigned long long)key);
+      if (prev == kEmpty64 || prev == key) return int64_t(s);
+      s = (s + 1) & mask;
+    }
+    atomicExch(overflow, 1);
+    return -1;
+  }
+
   __device__ __forceinline__ int64_t find_slot(uint64_t key) const {
     uint64_t s = home(key);
     for (uint64_t i = 0; i <= mask; ++i) {
@@ -130,6 +173,18 @@ struct Table64 {
   __device__ __forceinline__ int32_t find(uint64_t key) const {
     const int64_t s = find_slot(key);
     return s >= 0 ? vals[s] : -1;
+  }
+
+  // Split lookups, as Table32's.
+  __device__ __forceinline__ uint64_t word(uint64_t s) const { return keys[s]; }
+  __device__ __forceinline__ int64_t find_from(uint64_t s, uint64_t w, uint64_t key) const {
+    for (uint64_t i = 0; i <= mask; ++i) {
+      if (w == key) return int64_t(s);
+      if (w == kEmpty64) return -1;
+      s = (s + 1) & mask;
+      w = keys[s];
+    }
+    return -1;
   }
 
   __device__ __forceinline__ void set_value(int64_t slot, int32_t val) const { vals[slot] = val; }

@@ -3,13 +3,17 @@
 //
 // The reference finds neighbours by sorting the input keys and binary
 // searching every (offset, point) candidate (spconv_triton/pytorch/_impl/
-// pairs.py:196-220, pair_kernels.py:298-482).  Here the coordinates go into an
-// open-addressing hash table instead (32-bit keys packed with their row into
-// one 64-bit slot, or 64-bit keys with a side array of rows), and every output
-// row probes its kv neighbours directly ("output stationary"): each thread owns
-// one row and writes column r of every offset row of the table, so the stores
-// of a wave are contiguous, and the per-row offset bitmask comes out of the
-// same loop in registers.
+// pairs.py:196-220, pair_kernels.py:298-482).  Here the coordinates go into a
+// lookup structure instead -- for subm a dense cell -> row grid (small key
+// volumes) or a brick index (4-cell bricks in an open-addressing hash, each
+// with an occupancy mask and a popcount-ranked row list); for regular and
+// transposed convs an occupancy bitmap or an open-addressing hash of the
+// output keys (32-bit keys packed with their row into one 64-bit slot, or
+// 64-bit keys with a side array of rows) -- and every output row probes its kv
+// neighbours directly ("output stationary"): each thread owns one row and
+// writes column r of every offset row of the table, so the stores of a wave
+// are contiguous, and the per-row offset bitmask comes out of the same loop in
+// registers.
 //
 // Output order is the reference's, bit for bit:
 //  * subm: output rows are the input rows (pairs.py:400-401);
@@ -180,56 +184,21 @@ __device__ __forceinline__ bool subm_source_key(const GeomDev& g, const Coord& c
 template <class Table>
 using KeyInt = std::conditional_t<std::is_same_v<Table, Table32>, int32_t, int64_t>;
 
-__device__ __forceinline__ void odometer_next(const GeomDev& g, int* off) {
-  for (int d = g.ndim - 1; d >= 0; --d) {
-    if (++off[d] < g.ks[d]) return;
-    off[d] = 0;
+// (unrolled to 4 with a guard, so that `off` stays in registers)
+__device__ __forceinline__ void odometer_next(const GeomDev& g, int (&off)[4]) {
+  bool carry = true;
+#pragma unroll
+  for (int d = 3; d >= 0; --d) {
+    if (d < g.ndim && carry) {
+      if (++off[d] < g.ks[d]) carry = false;
+      else off[d] = 0;
+    }
   }
 }
 
 // ---------------------------------------------------------------------------
 // subm
 // ---------------------------------------------------------------------------
-template <class Table>
-__global__ __launch_bounds__(256) void subm_insert(const int32_t* __restrict__ idx, int64_t n,
-                                                   GeomDev g, Table t) {
-  const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (r >= n) return;
-  Coord c = load_coord(idx, r, g);
-  if (!c.ok) return;
-  int64_t acc = c.b;
-  for (int d = 0; d < g.ndim; ++d) acc = acc * g.in_shape[d] + c.x[d];
-  t.insert(uint64_t(acc), int32_t(r));
-}
-
-// One thread per output row r.  pf[k, r] = row of neighbour k, or -1;
-// pb[kv-1-k, r] = the same value (for odd kernels the subm relation is
-// symmetric: x_r + pad - off_k*dil == x_r - pad + off_{kv-1-k}*dil).
-template <class Table>
-__global__ __launch_bounds__(256) void subm_probe(const int32_t* __restrict__ idx, int64_t n,
-                                                  GeomDev g, Table t, int32_t* __restrict__ pf,
-                                                  int32_t* __restrict__ pb,
-                                                  uint32_t* __restrict__ words, int mic) {
-  const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (r >= n) return;
-  const Coord c = load_coord(idx, r, g);
-  int off[4] = {0, 0, 0, 0};
-  uint32_t word = 0;
-  for (int k = 0; k < g.kv; ++k) {
-    uint64_t key;
-    int32_t j = -1;
-    if (subm_source_key(g, c, off, &key)) j = t.find(key);
-    if (pf) pf[int64_t(k) * n + r] = j;
-    if (pb) pb[int64_t(g.kv - 1 - k) * n + r] = j;
-    if (j >= 0) word |= 1u << (k & 31);
-    if ((k & 31) == 31 || k == g.kv - 1) {
-      if (words) words[r * mic + (k >> 5)] = word;
-      word = 0;
-    }
-    odometer_next(g, off);
-  }
-}
-
 // ---- subm on a dense grid ---------------------------------------------------
 // When the key volume is small next to the number of rows, a dense cell -> row
 // array replaces the hash: filling it is cheaper than hashing, every probe is
@@ -550,6 +519,361 @@ static void conv_layout(W& w, const GeomDev& g, int64_t n, bool key64, ConvWs* o
   }
 }
 
+// ---- subm on a brick index (key volumes a dense grid does not fit) ----------
+// Above the dense grid's limits, every row's kv neighbours were separate
+// lookups in a coordinate hash, each a random probe chain: config 5 case 1
+// (4-D, ~500k rows, kv = 81) took 689 us for its rulebook probe.  Here the
+// coordinates are grouped into bricks of 4 cells along each of the last
+// min(ndim, 3) dimensions (at most 64 cells, one 64-bit occupancy mask), and
+// only bricks are hashed:
+//   * insert: every row sets its cell's bit in its brick's mask (the brick is
+//     inserted into the hash on first sight; its slot holds the mask);
+//   * bases: each slot's first entry in a compact row array, from a block scan
+//     of the masks' popcounts (one atomic per workgroup places the blocks:
+//     the positions depend on the order they run in, the lookups do not);
+//   * scatter: every row writes itself at base + popcount(mask below its
+//     cell), keeping the smallest row of a repeated coordinate (atomicMin, the
+//     rule of the other lookup structures);
+//   * probe: a row's window, 3 cells wide per dimension for a 3^D kernel,
+//     touches 1-2 bricks per bricked dimension; they are looked up once per
+//     slice of the leading (unbricked) dimensions into a per-thread LDS cache
+//     (at most kBrickWindow bricks; wider windows look each brick up as the
+//     offsets reach it, keeping the last one), and each offset is a bit test
+//     and a popcount rank.
+// Same results as the hash and the grid, bit for bit.
+constexpr int kBrickWindow = 8;  // bricks cached per row and leading slice
+
+struct BrickDev {
+  int nb;              // trailing dimensions cut into bricks of 4 cells
+  int64_t bshape[4];   // bricks per dimension (ceil(shape / 4) bricked, else shape)
+  uint64_t* masks;     // [cap] occupancy of the brick in hash slot s (bit = cell)
+  uint32_t* base;      // [cap] first entry of the slot's cells in rows
+  int32_t* rows;       // [n] row of each occupied cell
+  uint32_t* total;     // occupied cells (the base scan's running total)
+};
+
+static BrickDev brick_geom(const GeomDev& g) {
+  BrickDev b{};
+  b.nb = g.ndim < 3 ? g.ndim : 3;
+  for (int d = 0; d < g.ndim; ++d)
+    b.bshape[d] = d >= g.ndim - b.nb ? (g.in_shape[d] + 3) / 4 : g.in_shape[d];
+  return b;
+}
+
+// Brick volume (keys of the brick hash are below it).
+static double brick_volume(const GeomDev& g) {
+  const BrickDev b = brick_geom(g);
+  double v = double(g.batch);
+  for (int d = 0; d < g.ndim; ++d) v *= double(b.bshape[d]);
+  return v;
+}
+
+// Brick key and cell of an in-range coordinate.
+__device__ __forceinline__ void brick_of(const GeomDev& g, const BrickDev& bd, const Coord& c,
+                                         uint64_t* bkey, uint32_t* cell) {
+  int64_t acc = c.b;
+  uint32_t cl = 0;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    if (d < g.ndim) {
+      const bool bricked = d >= g.ndim - bd.nb;
+      acc = acc * bd.bshape[d] + (bricked ? (c.x[d] >> 2) : c.x[d]);
+      if (bricked) cl = cl * 4u + uint32_t(c.x[d] & 3);
+    }
+  }
+  *bkey = uint64_t(acc);
+  *cell = cl;
+}
+
+__global__ __launch_bounds__(256) void brick_fill(uint64_t* __restrict__ table, uint64_t cap,
+                                                  uint64_t* __restrict__ masks,
+                                                  int32_t* __restrict__ rows, int64_t n,
+                                                  uint32_t* __restrict__ total) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (uint64_t(i) < cap) {
+    table[i] = kEmpty64;
+    masks[i] = 0;
+  }
+  if (i < n) rows[i] = kNoRow;
+  if (i == 0) *total = 0;
+}
+
+template <class Table>
+__global__ __launch_bounds__(256) void brick_insert(const int32_t* __restrict__ idx, int64_t n,
+                                                    GeomDev g, Table t, BrickDev bd) {
+  const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const Coord c = load_coord(idx, r, g);
+  if (!c.ok) return;
+  uint64_t bkey;
+  uint32_t cell;
+  brick_of(g, bd, c, &bkey, &cell);
+  const int64_t s = t.insert_slot(bkey);
+  if (s >= 0) atomicOr(reinterpret_cast<unsigned long long*>(&bd.masks[s]), 1ull << cell);
+}
+
+constexpr int kBasePer = 8;  // slots per thread of brick_bases
+__global__ __launch_bounds__(256) void brick_bases(BrickDev bd, uint64_t cap) {
+  __shared__ uint32_t scan_lds[256 / 64 + 1];
+  __shared__ uint32_t s_first;
+  const uint64_t s0 = (uint64_t(blockIdx.x) * 256 + threadIdx.x) * kBasePer;
+  uint32_t cnt[kBasePer];
+  uint32_t sum = 0;
+#pragma unroll
+  for (int j = 0; j < kBasePer; ++j) {
+    cnt[j] = s0 + j < cap ? uint32_t(__popcll(bd.masks[s0 + j])) : 0u;
+    sum += cnt[j];
+  }
+  uint32_t tot;
+  uint32_t run = block_exclusive_scan<256>(sum, scan_lds, &tot);
+  if (threadIdx.x == 0) s_first = atomicAdd(bd.total, tot);
+  __syncthreads();
+  run += s_first;
+#pragma unroll
+  for (int j = 0; j < kBasePer; ++j) {
+    if (s0 + j < cap) bd.base[s0 + j] = run;
+    run += cnt[j];
+  }
+}
+
+template <class Table>
+__global__ __launch_bounds__(256) void brick_scatter(const int32_t* __restrict__ idx, int64_t n,
+                                                     GeomDev g, Table t, BrickDev bd) {
+  const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const Coord c = load_coord(idx, r, g);
+  if (!c.ok) return;
+  uint64_t bkey;
+  uint32_t cell;
+  brick_of(g, bd, c, &bkey, &cell);
+  const int64_t s = t.find_slot(bkey);
+  if (s < 0) return;  // (never: every row's brick was inserted)
+  const uint32_t pos =
+      bd.base[s] + uint32_t(__popcll(bd.masks[s] & ((uint64_t(1) << cell) - 1u)));
+  atomicMin(&bd.rows[pos], int32_t(r));
+}
+
+// One thread per output row, as subm_probe; the same outputs.  Latency is
+// what bounds a probe (its loads are random), so no load waits for another:
+// the hash lookups of a slice's window bricks have their home slots in
+// flight together, and the offsets go in batches of kBrickBatch whose rows'
+// positions come from the LDS cache first, then all their row loads, then
+// their stores.
+constexpr int kBrickBatch = 9;
+
+template <class Table>
+__global__ __launch_bounds__(256) void brick_probe(const int32_t* __restrict__ idx, int64_t n,
+                                                   GeomDev g, Table t, BrickDev bd,
+                                                   int32_t* __restrict__ pf,
+                                                   int32_t* __restrict__ pb,
+                                                   uint32_t* __restrict__ words, int mic) {
+  __shared__ uint64_t s_mask[kBrickWindow][256];
+  __shared__ uint32_t s_base[kBrickWindow][256];
+  const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n) return;  // (no barrier below: every LDS slot belongs to one thread)
+  const int tid = threadIdx.x;
+  const Coord c = load_coord(idx, r, g);
+  const int lead = g.ndim - bd.nb;
+  // the window's bricks along each bricked dimension: lo[d] .. lo[d] + nw[d] - 1
+  // (every loop over dimensions is unrolled to 4 with a guard, so the small
+  // arrays stay in registers)
+  int64_t lo[4] = {0, 0, 0, 0};
+  int nw[4] = {1, 1, 1, 1};
+  int W = 1;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    if (d < g.ndim && d >= lead) {
+      const int64_t c0 = c.x[d] - g.pad[d];
+      const int64_t c1 = c0 + int64_t(g.ks[d] - 1) * g.dil[d];
+      lo[d] = c0 >> 2;  // floor (arithmetic shift)
+      nw[d] = int((c1 >> 2) - lo[d] + 1);
+      W *= nw[d];
+    }
+  }
+  const bool cached = W <= kBrickWindow;
+  // brick key of brick coordinates bc (cell coordinates in the leading
+  // dimensions), or false when out of range
+  auto brick_key = [&](const int64_t (&bc)[4], uint64_t* key) -> bool {
+    int64_t acc = c.b;
+    bool ok = c.ok;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      if (d < g.ndim) {
+        ok = ok && bc[d] >= 0 && bc[d] < bd.bshape[d];
+        acc = acc * bd.bshape[d] + bc[d];
+      }
+    }
+    *key = uint64_t(acc);
+    return ok;
+  };
+  // the window's bricks of the leading slice holding cell coordinates q into
+  // the LDS cache; their lookups overlap
+  auto fill_window = [&](const int64_t (&q)[4]) {
+    uint64_t key[kBrickWindow], w[kBrickWindow];
+    bool ok[kBrickWindow];
+#pragma unroll
+    for (int e = 0; e < kBrickWindow; ++e) {
+      int64_t bc[4] = {0, 0, 0, 0};
+      int rem = e;
+#pragma unroll
+      for (int dd = 3; dd >= 0; --dd) {
+        if (dd < g.ndim) {
+          if (dd >= lead) {
+            bc[dd] = lo[dd] + rem % nw[dd];
+            rem /= nw[dd];
+          } else {
+            bc[dd] = q[dd];
+          }
+        }
+      }
+      ok[e] = e < W && brick_key(bc, &key[e]);
+      w[e] = ok[e] ? t.word(t.home(key[e])) : kEmpty64;
+    }
+    int64_t slot[kBrickWindow];
+#pragma unroll
+    for (int e = 0; e < kBrickWindow; ++e)
+      slot[e] = ok[e] ? t.find_from(t.home(key[e]), w[e], key[e]) : -1;
+#pragma unroll
+    for (int e = 0; e < kBrickWindow; ++e) {
+      if (e < W) {
+        s_mask[e][tid] = slot[e] >= 0 ? bd.masks[slot[e]] : 0ull;
+        s_base[e][tid] = slot[e] >= 0 ? bd.base[slot[e]] : 0u;
+      }
+    }
+  };
+  // offsets per leading slice (the bricked dimensions' kernel volume)
+  int kvb = 1;
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+    if (d < g.ndim && d >= lead) kvb *= g.ks[d];
+  int off[4] = {0, 0, 0, 0};
+  uint64_t last_key = ~uint64_t(0), last_mask = 0;  // the uncached path's one-brick cache
+  uint32_t last_base = 0;
+  uint32_t word = 0;
+  int k = 0;
+  for (int sl = 0; sl < g.kv / kvb; ++sl) {
+    if (cached) {  // the slice's window bricks (off holds its leading offsets, the rest 0)
+      int64_t q[4] = {0, 0, 0, 0};
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        if (d < g.ndim) q[d] = c.x[d] - g.pad[d] + int64_t(off[d]) * g.dil[d];
+      fill_window(q);
+    }
+    for (int b0 = 0; b0 < kvb; b0 += kBrickBatch) {
+      int32_t pos[kBrickBatch];  // entry of the batch's offsets in bd.rows, or -1
+#pragma unroll
+      for (int i = 0; i < kBrickBatch; ++i) {
+        pos[i] = -1;
+        if (b0 + i < kvb) {
+          int64_t q[4] = {0, 0, 0, 0};
+          bool ok = c.ok;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            if (d < g.ndim) {
+              q[d] = c.x[d] - g.pad[d] + int64_t(off[d]) * g.dil[d];
+              ok = ok && q[d] >= 0 && q[d] < g.in_shape[d];
+            }
+          }
+          if (ok) {
+            uint32_t cell = 0;
+            int e = 0;
+            int64_t bc[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              if (d < g.ndim) {
+                if (d >= lead) {
+                  cell = cell * 4u + uint32_t(q[d] & 3);
+                  e = e * nw[d] + int((q[d] >> 2) - lo[d]);
+                  bc[d] = q[d] >> 2;
+                } else {
+                  bc[d] = q[d];
+                }
+              }
+            }
+            uint64_t m;
+            uint32_t bs;
+            if (cached) {
+              m = s_mask[e][tid];
+              bs = s_base[e][tid];
+            } else {
+              uint64_t key;
+              brick_key(bc, &key);
+              if (key != last_key) {
+                const int64_t sk = t.find_slot(key);
+                last_mask = sk >= 0 ? bd.masks[sk] : 0ull;
+                last_base = sk >= 0 ? bd.base[sk] : 0u;
+                last_key = key;
+              }
+              m = last_mask;
+              bs = last_base;
+            }
+            if ((m >> cell) & 1u)
+              pos[i] = int32_t(bs + uint32_t(__popcll(m & ((uint64_t(1) << cell) - 1u))));
+          }
+          odometer_next(g, off);
+        }
+      }
+      int32_t j[kBrickBatch];
+#pragma unroll
+      for (int i = 0; i < kBrickBatch; ++i) j[i] = pos[i] >= 0 ? bd.rows[pos[i]] : -1;
+#pragma unroll
+      for (int i = 0; i < kBrickBatch; ++i) {
+        if (b0 + i < kvb) {
+          if (pf) pf[int64_t(k) * n + r] = j[i];
+          if (pb) pb[int64_t(g.kv - 1 - k) * n + r] = j[i];
+          if (j[i] >= 0) word |= 1u << (k & 31);
+          if ((k & 31) == 31 || k == g.kv - 1) {
+            if (words) words[r * mic + (k >> 5)] = word;
+            word = 0;
+          }
+          ++k;
+        }
+      }
+    }
+  }
+}
+
+template <class W>
+static void brick_layout(W& w, int64_t n, bool key64, BrickDev* bd, uint64_t** table, int** flags,
+                         uint64_t* cap_out) {
+  const uint64_t cap = table_capacity(n);
+  *flags = w.template take<int>(64);
+  uint32_t* total = w.template take<uint32_t>(64);
+  *table = w.template take<uint64_t>(cap);  // Table32 slots or Table64 keys
+  uint64_t* masks = w.template take<uint64_t>(cap);
+  uint32_t* base = w.template take<uint32_t>(cap);
+  int32_t* rows = w.template take<int32_t>(size_t(n));
+  (void)key64;
+  if (bd) {
+    bd->masks = masks;
+    bd->base = base;
+    bd->rows = rows;
+    bd->total = total;
+  }
+  *cap_out = cap;
+}
+
+template <class Table>
+static int run_brick_subm(const int32_t* indices, int64_t n, const GeomDev& d, Table t,
+                          const BrickDev& bd, uint64_t cap, uint64_t* table, int32_t* pair_fwd,
+                          int32_t* pair_bwd, uint32_t* mask_words, int mic, hipStream_t s) {
+  const int64_t fill = int64_t(cap) > n ? int64_t(cap) : n;
+  SP_CHECK_ARG(cdiv(fill, 256) <= kMaxGridX, "pairgen_subm: too many rows");
+  brick_fill<<<unsigned(cdiv(fill, 256)), 256, 0, s>>>(table, cap, bd.masks, bd.rows, n, bd.total);
+  SP_LAUNCHED();
+  const unsigned blocks = unsigned(cdiv(n, 256));
+  brick_insert<Table><<<blocks, 256, 0, s>>>(indices, n, d, t, bd);
+  SP_LAUNCHED();
+  brick_bases<<<unsigned(cdiv(int64_t(cap), 256 * kBasePer)), 256, 0, s>>>(bd, cap);
+  SP_LAUNCHED();
+  brick_scatter<Table><<<blocks, 256, 0, s>>>(indices, n, d, t, bd);
+  SP_LAUNCHED();
+  brick_probe<Table><<<blocks, 256, 0, s>>>(indices, n, d, t, bd, pair_fwd, pair_bwd, mask_words,
+                                            mic);
+  SP_LAUNCHED();
+  return SP_OK;
+}
+
 // ---- regular / transposed convs on an occupancy bitmap ------------------------
 // With int32 keys and an output key volume of at most kBitmapCellsPerRow cells
 // per input row, one bit per output cell replaces the hash, the key sort and
@@ -729,15 +1053,6 @@ struct WsSizerP {
   }
 };
 
-template <class W>
-static void subm_layout(W& w, int64_t n, bool key64, void** ta, int32_t** tv, int** flags,
-                        uint64_t* cap_out) {
-  const uint64_t cap = table_capacity(n);
-  *flags = w.template take<int>(64);
-  *ta = w.template take<uint64_t>(cap);
-  *tv = key64 ? w.template take<int32_t>(cap) : nullptr;
-  *cap_out = cap;
-}
 
 // counter[0]: unique keys; the candidates (the table's pairs) are counted
 // into *npairs.
@@ -952,11 +1267,10 @@ size_t sp_pairgen_workspace_size(const sp_geom* g, int64_t n) {
       z.take<int32_t>(size_t(subm_cells(d) + 2 * kGridPad));
       return z.off;
     }
-    void* ta;
-    int32_t* tv;
+    uint64_t* ta;
     int* fl;
     uint64_t cap;
-    subm_layout(z, n, key64, &ta, &tv, &fl, &cap);
+    brick_layout(z, n, key64, nullptr, &ta, &fl, &cap);
     return z.off;
   }
   WsSizerP z;
@@ -1007,29 +1321,19 @@ int sp_pairgen_subm(const sp_geom* g, const int32_t* indices, int64_t n, int32_t
     SP_LAUNCHED();
     return SP_OK;
   }
-  void* ta;
-  int32_t* tv;
+  // the brick index (bricks hashed with 32-bit keys while the brick volume
+  // allows, whatever the key width of the cells)
+  BrickDev bd = brick_geom(d);
+  uint64_t* table;
   int* flags;
   uint64_t cap;
-  subm_layout(c, n, key64, &ta, &tv, &flags, &cap);
-  rc = launch_fill_u64(static_cast<uint64_t*>(ta), int64_t(cap), kEmpty64, s);
-  if (rc) return rc;
-  if (key64) {
-    rc = launch_fill_i32(tv, int64_t(cap), 0x7fffffff, s);
-    if (rc) return rc;
-    Table64 t{static_cast<uint64_t*>(ta), tv, cap - 1, flags};
-    subm_insert<<<blocks, 256, 0, s>>>(indices, n, d, t);
-    SP_LAUNCHED();
-    subm_probe<<<blocks, 256, 0, s>>>(indices, n, d, t, pair_fwd, pair_bwd, mask_words, mic);
-    SP_LAUNCHED();
-  } else {
-    Table32 t{static_cast<uint64_t*>(ta), cap - 1, flags};
-    subm_insert<<<blocks, 256, 0, s>>>(indices, n, d, t);
-    SP_LAUNCHED();
-    subm_probe<<<blocks, 256, 0, s>>>(indices, n, d, t, pair_fwd, pair_bwd, mask_words, mic);
-    SP_LAUNCHED();
-  }
-  return SP_OK;
+  brick_layout(c, n, key64, &bd, &table, &flags, &cap);
+  (void)blocks;
+  if (brick_volume(d) < 2147483648.0)
+    return run_brick_subm(indices, n, d, Table32{table, cap - 1, flags}, bd, cap, table, pair_fwd,
+                          pair_bwd, mask_words, mic, s);
+  return run_brick_subm(indices, n, d, Table64{table, nullptr, cap - 1, flags}, bd, cap, table,
+                        pair_fwd, pair_bwd, mask_words, mic, s);
 }
 
 int64_t sp_pairgen_subm_grid_cells(const sp_geom* g, int64_t n) {

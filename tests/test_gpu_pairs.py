@@ -410,6 +410,96 @@ def test_mask_sort_stable_large(n, grid):
     assert _sort_drops() == 0, "a radix-sort scatter dropped positions"
 
 
+def _mask_sort(words, kv, split, ws, pm, ar):
+    from spconv_triton.pytorch._impl import _lib
+
+    n = words.shape[0]
+    _lib.check(_lib.lib().sp_mask_sort(_lib.ptr(words), n, 1, kv, split, 1, _lib.ptr(pm),
+                                       _lib.ptr(ar), _lib.ptr(ws), ws.numel(),
+                                       _lib.stream_of(words.device)), "sp_mask_sort")
+
+
+def _expect_sorted(w_np, split):
+    keys = w_np.astype(np.uint64) & np.uint64(split)
+    order = np.argsort(keys, kind="stable")
+    return order.astype(np.int64), keys[order].astype(np.int64)
+
+
+def test_mask_sort_single_launch_cases():
+    """Single-word mask sorts of up to 128 radix tiles run as one launch whose
+    tiles meet at device-wide barriers.  Against numpy's stable argsort: one
+    to 128 tiles (partial last tiles, a single row), 1 to 4 passes (kv 5, 9,
+    27, 32), a split mask, heavily repeated keys; every sort reuses one
+    workspace that starts as random bytes, so barrier flags left by the
+    previous sort (and garbage) sit in the buffer and must not be taken for the
+    current sort's."""
+    from spconv_triton.pytorch._impl import _lib
+
+    rng = np.random.default_rng(5)
+    L = _lib.lib()
+    n_max = 128 * 2048
+    ws = torch.from_numpy(rng.integers(0, 256, size=L.sp_mask_sort_workspace_size(n_max, 1),
+                                       dtype=np.uint8)).to(DEV)
+    cases = [(1, 27, 0xFFFFFFFF), (100, 9, 0xFFFFFFFF), (2048, 27, 0xFFFFFFFF),
+             (2049, 5, 0xFFFFFFFF), (5000, 32, 0xFFFFFFFF), (70_001, 27, 0x3FFF),
+             (131_072, 18, 0xFFFFFFFF), (n_max - 3, 27, 0xFFFFFFFF), (n_max, 32, 0xFFFF0000)]
+    for n, kv, split in cases:
+        hi = (1 << kv) - 1
+        w_np = rng.integers(0, hi + 1, size=n, dtype=np.int64)
+        w_np[rng.random(n) < 0.5] &= 0x7  # many equal keys: stability matters
+        words = torch.from_numpy(w_np.astype(np.uint32).view(np.int32)).to(DEV)
+        pm = torch.empty(n, dtype=torch.int32, device=DEV)
+        ar = torch.empty(n, dtype=torch.int32, device=DEV)
+        _mask_sort(words, kv, split, ws, pm, ar)
+        order, keys = _expect_sorted(w_np, split)
+        np.testing.assert_array_equal(ar.cpu().numpy(), order, f"argsort n={n} kv={kv}")
+        np.testing.assert_array_equal(pm.cpu().numpy().astype(np.int64) & 0xFFFFFFFF, keys,
+                                      f"sorted words n={n} kv={kv}")
+    assert _sort_drops() == 0, "a sort scatter dropped positions or a barrier timed out"
+
+
+def test_mask_sort_graph_replays():
+    """The single-launch mask sort captured into a HIP graph: every replay (new
+    words copied in between, eager sorts on the same workspace between replays)
+    equals numpy's stable argsort -- each launch, replays included, takes a new
+    barrier epoch."""
+    from spconv_triton.pytorch._impl import _lib
+
+    rng = np.random.default_rng(9)
+    L = _lib.lib()
+    n, kv = 150_000, 27
+    ws = torch.empty(L.sp_mask_sort_workspace_size(n, 1), dtype=torch.uint8, device=DEV)
+    words = torch.zeros(n, dtype=torch.int32, device=DEV)
+    pm = torch.empty(n, dtype=torch.int32, device=DEV)
+    ar = torch.empty(n, dtype=torch.int32, device=DEV)
+    _mask_sort(words, kv, 0xFFFFFFFF, ws, pm, ar)  # warm-up
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            _mask_sort(words, kv, 0xFFFFFFFF, ws, pm, ar)
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(3):
+        w_np = rng.integers(0, 1 << kv, size=n, dtype=np.int64)
+        w_np[rng.random(n) < 0.3] = 5
+        words.copy_(torch.from_numpy(w_np.astype(np.int32)))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        order, keys = _expect_sorted(w_np, 0xFFFFFFFF)
+        np.testing.assert_array_equal(ar.cpu().numpy(), order, f"replay {rep}")
+        np.testing.assert_array_equal(pm.cpu().numpy().astype(np.int64) & 0xFFFFFFFF, keys)
+        # an eager sort on the same workspace between replays
+        pm2 = torch.empty_like(pm)
+        ar2 = torch.empty_like(ar)
+        _mask_sort(words, kv, 0xFFFFFFFF, ws, pm2, ar2)
+        torch.cuda.synchronize()
+        assert torch.equal(ar2, ar) and torch.equal(pm2, pm)
+    assert _sort_drops() == 0
+
+
 def _sort_drops() -> int:
     """Positions the radix-sort scatters dropped since the last call (0 for
     consistent histograms), then reset."""
