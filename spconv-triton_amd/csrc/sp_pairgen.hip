@@ -833,6 +833,132 @@ __global__ __launch_bounds__(256) void brick_probe(const int32_t* __restrict__ i
   }
 }
 
+// brick_probe for the usual window: 3 cells (dilation 1) along each of the
+// three bricked dimensions, NDIM = 3, or 4 with any leading kernel size and
+// dilation.  The window's per-dimension cells (valid, cell in brick, which of
+// its 1-2 bricks) are computed once per row, so each of a slice's 27 offsets
+// is a handful of register operations; the same outputs.
+template <class Table, int NDIM>
+__global__ __launch_bounds__(256) void brick_probe3(const int32_t* __restrict__ idx, int64_t n,
+                                                    GeomDev g, Table t, BrickDev bd,
+                                                    int32_t* __restrict__ pf,
+                                                    int32_t* __restrict__ pb,
+                                                    uint32_t* __restrict__ words, int mic) {
+  static_assert(NDIM == 3 || NDIM == 4, "three bricked dimensions, at most one leading");
+  constexpr int LEAD = NDIM - 3;
+  __shared__ uint64_t s_mask[kBrickWindow][256];
+  __shared__ uint32_t s_base[kBrickWindow][256];
+  const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= n) return;  // (no barrier below: every LDS slot belongs to one thread)
+  const int tid = threadIdx.x;
+  const Coord c = load_coord(idx, r, g);
+  // per bricked dimension d and window position o (cell x - 1 + o): in range,
+  // cell index in its brick, and whether it lies in the window's second brick
+  int64_t lo[3];
+  int nw[3];
+  bool vin[3][3];
+  uint32_t cc[3][3], eb[3][3];
+#pragma unroll
+  for (int d = 0; d < 3; ++d) {
+    const int64_t x = c.x[LEAD + d];
+    lo[d] = (x - 1) >> 2;
+    nw[d] = int(((x + 1) >> 2) - lo[d] + 1);
+#pragma unroll
+    for (int o = 0; o < 3; ++o) {
+      const int64_t v = x - 1 + o;
+      vin[d][o] = v >= 0 && v < g.in_shape[LEAD + d];
+      cc[d][o] = uint32_t(v & 3);
+      eb[d][o] = uint32_t((v >> 2) - lo[d]);
+    }
+  }
+  const int ns = LEAD ? g.ks[0] : 1;  // leading slices
+  uint32_t word = 0;
+#pragma unroll 1
+  for (int sl = 0; sl < ns; ++sl) {
+    int64_t q0 = 0;
+    bool slice_ok = c.ok;
+    if (LEAD) {
+      q0 = c.x[0] - g.pad[0] + int64_t(sl) * g.dil[0];
+      slice_ok = slice_ok && q0 >= 0 && q0 < g.in_shape[0];
+    }
+    // the slice's window bricks (i, j, l) in {0, 1}^3 into the LDS cache
+    {
+      uint64_t key[kBrickWindow], w[kBrickWindow];
+      bool ok[kBrickWindow];
+#pragma unroll
+      for (int e = 0; e < kBrickWindow; ++e) {
+        const int i = e >> 2, j = (e >> 1) & 1, l = e & 1;
+        const int64_t b0 = lo[0] + i, b1 = lo[1] + j, b2 = lo[2] + l;
+        ok[e] = slice_ok && i < nw[0] && j < nw[1] && l < nw[2] && b0 >= 0 &&
+                b0 < bd.bshape[LEAD] && b1 >= 0 && b1 < bd.bshape[LEAD + 1] && b2 >= 0 &&
+                b2 < bd.bshape[LEAD + 2];
+        int64_t acc = c.b;
+        if (LEAD) acc = acc * bd.bshape[0] + q0;
+        acc = ((acc * bd.bshape[LEAD] + b0) * bd.bshape[LEAD + 1] + b1) * bd.bshape[LEAD + 2] +
+              b2;
+        key[e] = uint64_t(acc);
+        w[e] = ok[e] ? t.word(t.home(key[e])) : kEmpty64;
+      }
+      int64_t slot[kBrickWindow];
+#pragma unroll
+      for (int e = 0; e < kBrickWindow; ++e)
+        slot[e] = ok[e] ? t.find_from(t.home(key[e]), w[e], key[e]) : -1;
+#pragma unroll
+      for (int e = 0; e < kBrickWindow; ++e) {
+        s_mask[e][tid] = slot[e] >= 0 ? bd.masks[slot[e]] : 0ull;
+        s_base[e][tid] = slot[e] >= 0 ? bd.base[slot[e]] : 0u;
+      }
+    }
+    // the 27 offsets, 9 at a time (one plane of the first bricked dimension)
+#pragma unroll
+    for (int oz = 0; oz < 3; ++oz) {
+      int32_t pos[9];
+#pragma unroll
+      for (int oy = 0; oy < 3; ++oy) {
+#pragma unroll
+        for (int ox = 0; ox < 3; ++ox) {
+          const bool ok = slice_ok && vin[0][oz] && vin[1][oy] && vin[2][ox];
+          const uint32_t cell = cc[0][oz] * 16u + cc[1][oy] * 4u + cc[2][ox];
+          const uint32_t e = eb[0][oz] * 4u + eb[1][oy] * 2u + eb[2][ox];
+          int32_t p = -1;
+          if (ok) {
+            const uint64_t m = s_mask[e][tid];
+            if ((m >> cell) & 1u)
+              p = int32_t(s_base[e][tid] + uint32_t(__popcll(m & ((uint64_t(1) << cell) - 1u))));
+          }
+          pos[oy * 3 + ox] = p;
+        }
+      }
+      int32_t jr[9];
+#pragma unroll
+      for (int i = 0; i < 9; ++i) jr[i] = pos[i] >= 0 ? bd.rows[pos[i]] : -1;
+      // offset k = sl * 27 + oz * 9 + i: pf row k, pb row kv - 1 - k
+      const int k0 = sl * 27 + oz * 9;
+      int32_t* pfk = pf ? pf + int64_t(k0) * n + r : nullptr;
+      int32_t* pbk = pb ? pb + int64_t(g.kv - 1 - k0) * n + r : nullptr;
+#pragma unroll
+      for (int i = 0; i < 9; ++i) {
+        const int k = k0 + i;
+        if (pf) pfk[int64_t(i) * n] = jr[i];
+        if (pb) pbk[-int64_t(i) * n] = jr[i];
+        if (jr[i] >= 0) word |= 1u << (k & 31);
+        if ((k & 31) == 31 || k == g.kv - 1) {
+          if (words) words[r * mic + (k >> 5)] = word;
+          word = 0;
+        }
+      }
+    }
+  }
+}
+
+// Whether brick_probe3 serves this geometry.
+static bool brick_probe3_ok(const GeomDev& g) {
+  if (g.ndim != 3 && g.ndim != 4) return false;
+  for (int d = g.ndim - 3; d < g.ndim; ++d)
+    if (g.ks[d] != 3 || g.dil[d] != 1) return false;
+  return true;
+}
+
 template <class W>
 static void brick_layout(W& w, int64_t n, bool key64, BrickDev* bd, uint64_t** table, int** flags,
                          uint64_t* cap_out) {
@@ -868,8 +994,15 @@ static int run_brick_subm(const int32_t* indices, int64_t n, const GeomDev& d, T
   SP_LAUNCHED();
   brick_scatter<Table><<<blocks, 256, 0, s>>>(indices, n, d, t, bd);
   SP_LAUNCHED();
-  brick_probe<Table><<<blocks, 256, 0, s>>>(indices, n, d, t, bd, pair_fwd, pair_bwd, mask_words,
-                                            mic);
+  if (brick_probe3_ok(d) && d.ndim == 3)
+    brick_probe3<Table, 3><<<blocks, 256, 0, s>>>(indices, n, d, t, bd, pair_fwd, pair_bwd,
+                                                   mask_words, mic);
+  else if (brick_probe3_ok(d))
+    brick_probe3<Table, 4><<<blocks, 256, 0, s>>>(indices, n, d, t, bd, pair_fwd, pair_bwd,
+                                                   mask_words, mic);
+  else
+    brick_probe<Table><<<blocks, 256, 0, s>>>(indices, n, d, t, bd, pair_fwd, pair_bwd,
+                                              mask_words, mic);
   SP_LAUNCHED();
   return SP_OK;
 }

@@ -34,6 +34,9 @@ GEOMS = [
     ([16, 16, 16], [5, 5, 5], [1] * 3, [2] * 3, [1] * 3, [0] * 3, True, False),
     ([16, 16, 16], [5, 5, 5], [2] * 3, [2] * 3, [1] * 3, [0] * 3, False, False),
     ([16, 16, 16], [2, 2, 2], [2] * 3, [0] * 3, [1] * 3, [0] * 3, False, False),
+    # 4-D subm whose leading dimension has kernel 5 and dilation 2 (the
+    # brick index's 3x3x3 probe then runs 5 leading slices)
+    ([9, 8, 7, 6], [5, 3, 3, 3], [1] * 4, [4, 1, 1, 1], [2, 1, 1, 1], [0] * 4, True, False),
 ]
 
 
