@@ -588,13 +588,15 @@ __device__ __forceinline__ void brick_of(const GeomDev& g, const BrickDev& bd, c
 __global__ __launch_bounds__(256) void brick_fill(uint64_t* __restrict__ table, uint64_t cap,
                                                   uint64_t* __restrict__ masks,
                                                   int32_t* __restrict__ rows, int64_t n,
-                                                  uint32_t* __restrict__ total) {
+                                                  uint32_t* __restrict__ total,
+                                                  uint32_t* __restrict__ words, int64_t n_words) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (uint64_t(i) < cap) {
     table[i] = kEmpty64;
     masks[i] = 0;
   }
   if (i < n) rows[i] = kNoRow;
+  if (i < n_words) words[i] = 0;  // (the slice-parallel probe ORs into them)
   if (i == 0) *total = 0;
 }
 
@@ -837,7 +839,11 @@ __global__ __launch_bounds__(256) void brick_probe(const int32_t* __restrict__ i
 // three bricked dimensions, NDIM = 3, or 4 with any leading kernel size and
 // dilation.  The window's per-dimension cells (valid, cell in brick, which of
 // its 1-2 bricks) are computed once per row, so each of a slice's 27 offsets
-// is a handful of register operations; the same outputs.
+// is a handful of register operations; the same outputs.  NDIM = 4: one
+// thread per (leading slice, row), slice-major, so that the kernel keeps the
+// 3-D instance's registers (a loop over the slices in one thread needed 232
+// VGPRs); the threads of a row OR their bits into its mask words, which
+// brick_fill zeroed.
 template <class Table, int NDIM>
 __global__ __launch_bounds__(256) void brick_probe3(const int32_t* __restrict__ idx, int64_t n,
                                                     GeomDev g, Table t, BrickDev bd,
@@ -848,8 +854,11 @@ __global__ __launch_bounds__(256) void brick_probe3(const int32_t* __restrict__ 
   constexpr int LEAD = NDIM - 3;
   __shared__ uint64_t s_mask[kBrickWindow][256];
   __shared__ uint32_t s_base[kBrickWindow][256];
-  const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (r >= n) return;  // (no barrier below: every LDS slot belongs to one thread)
+  const int ns = LEAD ? g.ks[0] : 1;  // leading slices
+  const int64_t tg = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (tg >= n * ns) return;  // (no barrier below: every LDS slot belongs to one thread)
+  const int64_t r = LEAD ? tg % n : tg;
+  const int sl = LEAD ? int(tg / n) : 0;
   const int tid = threadIdx.x;
   const Coord c = load_coord(idx, r, g);
   // per bricked dimension d and window position o (cell x - 1 + o): in range,
@@ -871,10 +880,8 @@ __global__ __launch_bounds__(256) void brick_probe3(const int32_t* __restrict__ 
       eb[d][o] = uint32_t((v >> 2) - lo[d]);
     }
   }
-  const int ns = LEAD ? g.ks[0] : 1;  // leading slices
   uint32_t word = 0;
-#pragma unroll 1
-  for (int sl = 0; sl < ns; ++sl) {
+  {
     int64_t q0 = 0;
     bool slice_ok = c.ok;
     if (LEAD) {
@@ -942,8 +949,16 @@ __global__ __launch_bounds__(256) void brick_probe3(const int32_t* __restrict__ 
         if (pf) pfk[int64_t(i) * n] = jr[i];
         if (pb) pbk[-int64_t(i) * n] = jr[i];
         if (jr[i] >= 0) word |= 1u << (k & 31);
-        if ((k & 31) == 31 || k == g.kv - 1) {
-          if (words) words[r * mic + (k >> 5)] = word;
+        // a slice's last offset ends its bits too (NDIM = 4: other slices'
+        // threads fill the rest of the word)
+        if ((k & 31) == 31 || k == g.kv - 1 || (LEAD && k == sl * 27 + 26)) {
+          if (words) {
+            if (LEAD) {
+              if (word) atomicOr(&words[r * mic + (k >> 5)], word);
+            } else {
+              words[r * mic + (k >> 5)] = word;
+            }
+          }
           word = 0;
         }
       }
@@ -983,9 +998,13 @@ template <class Table>
 static int run_brick_subm(const int32_t* indices, int64_t n, const GeomDev& d, Table t,
                           const BrickDev& bd, uint64_t cap, uint64_t* table, int32_t* pair_fwd,
                           int32_t* pair_bwd, uint32_t* mask_words, int mic, hipStream_t s) {
-  const int64_t fill = int64_t(cap) > n ? int64_t(cap) : n;
+  const bool slices = brick_probe3_ok(d) && d.ndim == 4;  // the slice-parallel probe
+  const int64_t n_words = slices && mask_words ? n * mic : 0;
+  int64_t fill = int64_t(cap) > n ? int64_t(cap) : n;
+  fill = fill > n_words ? fill : n_words;
   SP_CHECK_ARG(cdiv(fill, 256) <= kMaxGridX, "pairgen_subm: too many rows");
-  brick_fill<<<unsigned(cdiv(fill, 256)), 256, 0, s>>>(table, cap, bd.masks, bd.rows, n, bd.total);
+  brick_fill<<<unsigned(cdiv(fill, 256)), 256, 0, s>>>(table, cap, bd.masks, bd.rows, n, bd.total,
+                                                       mask_words, n_words);
   SP_LAUNCHED();
   const unsigned blocks = unsigned(cdiv(n, 256));
   brick_insert<Table><<<blocks, 256, 0, s>>>(indices, n, d, t, bd);
@@ -997,9 +1016,11 @@ static int run_brick_subm(const int32_t* indices, int64_t n, const GeomDev& d, T
   if (brick_probe3_ok(d) && d.ndim == 3)
     brick_probe3<Table, 3><<<blocks, 256, 0, s>>>(indices, n, d, t, bd, pair_fwd, pair_bwd,
                                                    mask_words, mic);
-  else if (brick_probe3_ok(d))
-    brick_probe3<Table, 4><<<blocks, 256, 0, s>>>(indices, n, d, t, bd, pair_fwd, pair_bwd,
-                                                   mask_words, mic);
+  else if (slices) {
+    SP_CHECK_ARG(cdiv(n * d.ks[0], 256) <= kMaxGridX, "pairgen_subm: too many rows");
+    brick_probe3<Table, 4><<<unsigned(cdiv(n * d.ks[0], 256)), 256, 0, s>>>(
+        indices, n, d, t, bd, pair_fwd, pair_bwd, mask_words, mic);
+  }
   else
     brick_probe<Table><<<blocks, 256, 0, s>>>(indices, n, d, t, bd, pair_fwd, pair_bwd,
                                               mask_words, mic);
