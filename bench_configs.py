@@ -186,6 +186,8 @@ def _cached_layer(conv, idx, shape, C, reps):
             pairs = int((rb.pair_fwd >= 0).sum().item())
         else:  # Native rulebook: per-offset pair counts
             pairs = int(rb.indice_pair_num.sum().item())
+            if rb.is_subm:  # it lists the offsets before the centre only (symmetry)
+                pairs = 2 * pairs + int(rb.out_indices.shape[0])
         xc = spconv.SparseConvTensor(feats, it, shape, bs, indice_dict=y.indice_dict)
         for _ in range(5):
             conv(xc)

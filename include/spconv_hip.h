@@ -226,8 +226,10 @@ int sp_conv_gemm_packed(const void* a, int32_t dtype, int64_t n_src, const void*
  * table, like the reference memoises its tables on the indice data
  * (spconv_triton/pytorch/_impl/pairs.py:429-469 native_pair_to_tables,
  * gemm.py:661-669 valid_signal).  No reference entry point corresponds to it.
- * sp_gather_plan_bytes returns 0 when kv is outside 1..64 (no plan: use
- * sp_conv_gemm_packed).  sp_gather_plan_build is asynchronous; n_overflow
+ * sp_gather_plan_bytes returns 0 when kv is outside 1..1024 (no plan: use
+ * sp_conv_gemm_packed).  A tile lists at most 64 offsets with a pair among
+ * its rows; a tile with more is gathered directly, like one whose rows do not
+ * fit in LDS (an overflow tile).  sp_gather_plan_build is asynchronous; n_overflow
  * (nullable) requests the number of tiles whose distinct rows do not fit in
  * LDS (the GEMM gathers those directly from memory), which costs one stream
  * synchronization.  row_words (nullable): the rows' mask words, words_per_row
@@ -251,7 +253,7 @@ int sp_conv_gemm_planned(const void* a, int32_t dtype, int64_t n_src, const void
 /* The gather-GEMM with the output rows taken in a given order: tile row i is
  * output row row_order[i] (a permutation of 0..M-1, here the stable mask
  * argsort), pairs_perm is the table permuted by it (sp_permute_table) and
- * plan (nullable, kv <= 64) a gather plan of pairs_perm.  Results are
+ * plan (nullable, kv <= 1024) a gather plan of pairs_perm.  Results are
  * bit-identical to the natural order's.  This is the reference's masked
  * traversal, which visits rows in mask_argsort order so that a row tile holds
  * rows with similar masks (gemm.py:282-296, the mask_argsort operand of

@@ -61,6 +61,8 @@ constexpr uint32_t kBOob = 0x80000000u;    // B offset of padding items
 constexpr uint32_t kColOob = 0x40000000u;  // B column offset of columns >= N
 constexpr uint32_t kMaxBtBytes = 0x40000000u;  // packed weights must stay below (host check)
 constexpr int kGroupOffsets = 64;          // kernel offsets per group (direct kernel)
+static_assert(kGroupOffsets == kPlanGroupOffsets,
+              "planned tiles keep their items in one group of the direct kernel");
 constexpr uint32_t kSlabBytes = 4096;      // B of one item: 4 pieces x 64 columns x 16 B
 constexpr int kPad = 7;                    // padding items after a direct-kernel item list
 
@@ -696,7 +698,9 @@ __host__ __device__ inline StagedLds staged_lds(int E, uint32_t out_size) {
 }
 
 // Every tile of a planned call (kv <= kPlanMaxKv): staged when its distinct
-// rows fit in LDS, else (an overflow tile) by the direct path.  ORDERED as
+// rows fit in LDS and its items (at most kPlanMaxItems, in one group of
+// kGroupOffsets offsets) are listed, else (an overflow tile) by the direct
+// path.  ORDERED as
 // for the direct kernel.
 template <typename T, typename OutT, bool VEC, bool ORDERED>
 __global__ __launch_bounds__(256, 2) void gather_gemm_staged(

@@ -568,7 +568,7 @@ static int launch_staged(dim3 grid, hipStream_t s, const T* A, const T* bt, cons
                       : gather_gemm_staged<T, OutT, VEC, false>;
   static bool attr_set[2] = {false, false};  // per kernel instance
   int rc = allow_lds(reinterpret_cast<const void*>(kern),
-                     staged_kernel_lds(kPlanMaxKv, kPlanMaxKv, uint32_t(sizeof(OutT))),
+                     staged_kernel_lds(plan_layout(1, kPlanMaxKv).E, kPlanMaxKv, uint32_t(sizeof(OutT))),
                      attr_set[c.order ? 1 : 0]);
   if (rc) return rc;
   kern<<<grid, 256, lds, s>>>(A, bt, pairs, c.order, c.plan, c.bias, o, nb, c.n_src, c.M, c.N,

@@ -10,17 +10,22 @@
 // there.  A plan holds what it needs for that, computed once per table:
 //   * per tile: U and the ascending list of distinct source rows;
 //   * per tile: the offsets with at least one pair among its rows ("items",
-//     ascending), which the GEMM takes in groups of kItemGroup;
+//     ascending), which the GEMM takes in groups of kItemGroup; at most
+//     kPlanMaxItems, all in one group of kPlanGroupOffsets offsets (a tile
+//     with more, or spanning two groups, is an overflow tile, below);
 //   * for every (item, row) the LDS byte address of the row's staged chunk
 //     (chunk_base(slot); the zero row for a row without a pair, a row past M
 //     and the items that fill up the tile's last group).
 //
-// Layout of one plan buffer (256-byte aligned parts), E = kv rounded up to a
-// multiple of kItemGroup:
+// Layout of one plan buffer (256-byte aligned parts), E = min(kv, kPlanMaxItems)
+// rounded up to a multiple of kItemGroup:
 //   n_overflow                  int32   number of overflow tiles (below)
 //   count[ntiles]               int32   U of the tile; U >= kLdsRows marks an
 //                                       overflow tile, whose rows do not fit in
-//                                       LDS (nothing else is written for it)
+//                                       LDS or whose items are more than
+//                                       kPlanMaxItems or span two groups of
+//                                       kPlanGroupOffsets (nothing else is
+//                                       written for it)
 //   overflow[ntiles]            int32   ascending ids of the overflow tiles
 //   rows[ntiles][kLdsRows]      int32   ascending distinct source rows, then -1
 //   nact[ntiles]                int32   items of the tile
@@ -40,7 +45,13 @@ namespace sp {
 
 constexpr int kTileRows = 256;      // output rows per GEMM workgroup (4 waves x 64)
 constexpr int kLdsRows = 896;       // staged rows per tile, including one zero row
-constexpr int kPlanMaxKv = 64;      // kTileRows * 64 = 16384 entries sorted in LDS
+constexpr int kPlanMaxItems = 64;   // items per tile: kTileRows * 64 = 16384 entries sorted in LDS
+constexpr int kPlanDenseKv = 64;    // kv up to which the builder reads every offset's entries
+constexpr int kPlanMaxKv = 1024;    // kv range of plans (above kPlanDenseKv: live offsets first)
+// The direct kernel sums a row's offsets 64 at a time (each group over all
+// reduction chunks), the planned kernels their items chunk by chunk: the two
+// orders agree, bit for bit, when a tile's items lie in one such group.
+constexpr int kPlanGroupOffsets = 64;
 constexpr int kItemGroup = 4;       // the GEMM runs whole groups of items
 constexpr int kChunkBytes = 64;     // one MFMA K-step of one row (32 f16/bf16 or 16 f32)
 constexpr int kSwizzleShift = 2;    // piece p of a row sits at piece p ^ ((slot >> 2) & 3)
@@ -66,7 +77,8 @@ inline PlanLayout plan_layout(int64_t M, int64_t kv) {
   PlanLayout p;
   const int64_t m = M > 0 ? M : 1;
   p.ntiles = cdiv(m, kTileRows);
-  p.E = int((kv + kItemGroup - 1) / kItemGroup * kItemGroup);
+  const int64_t items = kv < kPlanMaxItems ? kv : kPlanMaxItems;
+  p.E = int((items + kItemGroup - 1) / kItemGroup * kItemGroup);
   const size_t nt = size_t(p.ntiles);
   p.count_off = 256;
   p.overflow_off = align_up(p.count_off + nt * 4, 256);

@@ -14,7 +14,12 @@
 //     (no pair = INT32_MAX sorts last), the distinct values are compacted in
 //     place, and every entry's rank is found by binary search.
 // Both give U and the ascending distinct list; the tile's items are numbered
-// and every (item, row) gets the staged LDS address of its rank.  A second,
+// and every (item, row) gets the staged LDS address of its rank.
+// With kv above kPlanDenseKv (COMPACT) the tile's live offsets are found
+// first (from the rows' mask words, or by a scan of the tile's entries that
+// keeps only one bit per offset), numbered as items, and only their entries
+// are read: at most kPlanMaxItems of them, in one group of kPlanGroupOffsets,
+// a tile with more or spanning two groups being an overflow tile.  A second,
 // single-workgroup kernel lists the tiles whose rows do not fit in LDS; their
 // number is copied back to the host (the build's one synchronisation), so
 // that a GEMM launches the direct-gather kernel for them only when there are
@@ -26,7 +31,7 @@ namespace sp {
 
 constexpr int kPlanThreads = 512;
 
-template <int NP>
+template <int NP, bool COMPACT>
 __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
     const int32_t* __restrict__ pairs, int64_t M, int kv, int64_t n_src,
     int32_t* __restrict__ count, int32_t* __restrict__ rows_out, int32_t* __restrict__ nact_out,
@@ -36,34 +41,102 @@ __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
   // word rank offsets
   __shared__ int32_t keys[NP];
   __shared__ uint32_t scan_lds[kPlanThreads / 64 + 1];
-  __shared__ int32_t s_item[kPlanMaxKv];  // item number of offset k in the tile, or -1
+  // dense: item number of offset k in the tile, or -1; COMPACT: offset of item i
+  __shared__ int32_t s_item[kPlanMaxItems];
   __shared__ int32_t s_red[2][kPlanThreads / 64];
   __shared__ int32_t s_nact;
   constexpr int PER = NP / kPlanThreads;
   static_assert(PER <= 32, "first-occurrence flags are kept in one 32-bit mask");
+  static_assert(kPlanDenseKv <= kPlanMaxItems && kPlanMaxItems <= 64,
+                "one wave numbers the items");
+  static_assert(!COMPACT || NP >= kTileRows * kPlanMaxItems, "a tile's entries fit in NP");
   constexpr int32_t kNone = 0x7fffffff;
   constexpr int kBmWords = NP / 2;
   const int tid = threadIdx.x;
   const int64_t tile = blockIdx.x;
   const int64_t r0 = tile * kTileRows;
-  const int n_ent = kTileRows * kv;
 
-  // with the rows' mask words, the offsets no row of the tile has are not read
-  __shared__ uint32_t s_live[2];
-  if (tid < kPlanMaxKv) s_item[tid] = -1;
-  if (tid < 2) s_live[tid] = words ? 0u : 0xffffffffu;
+  // live offsets: with the rows' mask words, the offsets no row of the tile
+  // has are not read (dense: 2 words; COMPACT: up to kPlanMaxKv / 32)
+  constexpr int kLiveWords = COMPACT ? kPlanMaxKv / 32 : 2;
+  __shared__ uint32_t s_live[kLiveWords];
+  const int nlw = COMPACT ? (kv + 31) / 32 : 2;
+  if (tid < kPlanMaxItems) s_item[tid] = -1;
+  if (tid < nlw) s_live[tid] = (words || COMPACT) ? 0u : 0xffffffffu;
   __syncthreads();
   if (words) {  // (uniform)
     const int64_t r = r0 + tid;
     if (tid < kTileRows && r < M) {
       const uint32_t* wr = words + r * int64_t(mic);
-      const uint32_t w0 = wr[0], w1 = mic > 1 ? wr[1] : 0u;
-      if (w0) atomicOr(&s_live[0], w0);
-      if (w1) atomicOr(&s_live[1], w1);
+      if (COMPACT) {
+        for (int j = 0; j < nlw; ++j) {
+          const uint32_t w = wr[j];
+          if (w) atomicOr(&s_live[j], w);
+        }
+      } else {
+        const uint32_t w0 = wr[0], w1 = mic > 1 ? wr[1] : 0u;
+        if (w0) atomicOr(&s_live[0], w0);
+        if (w1) atomicOr(&s_live[1], w1);
+      }
+    }
+    __syncthreads();
+  } else if (COMPACT) {
+    // scan: wave w reads offsets w / 4, w / 4 + 2, ... of its 64 rows, and
+    // one lane per offset sets its bit if any of them has a pair
+    const int lr = tid & (kTileRows - 1), k0 = tid / kTileRows;
+    const int64_t r = r0 + lr;
+    constexpr int kScanStep = kPlanThreads / kTileRows;
+    constexpr int kBatch = 8;
+    for (int kb = k0; kb < kv; kb += kScanStep * kBatch) {
+      int32_t x[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int k = kb + j * kScanStep;
+        x[j] = (k < kv && r < M) ? pairs[int64_t(k) * M + r] : -1;
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int k = kb + j * kScanStep;
+        const bool any = __builtin_amdgcn_ballot_w64(x[j] >= 0 && x[j] < n_src) != 0;
+        if (any && (tid & 63) == 0) atomicOr(&s_live[k >> 5], 1u << (k & 31));
+      }
     }
     __syncthreads();
   }
-  const uint64_t live = (uint64_t(s_live[1]) << 32) | s_live[0];
+  if (COMPACT) {
+    // items: the live offsets ascending, numbered by one wave (a scan of the
+    // words' popcounts); more than kPlanMaxItems, or items in two groups of
+    // kPlanGroupOffsets, make an overflow tile
+    if (tid < 64) {
+      uint32_t w = tid < nlw ? s_live[tid] : 0u;
+      if (tid == nlw - 1 && (kv & 31)) w &= (1u << (kv & 31)) - 1u;
+      const int c = __builtin_popcount(w);
+      int incl = c;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int o = __shfl_up(incl, off, 64);
+        if (tid >= off) incl += o;
+      }
+      int pos = incl - c;
+      while (w) {
+        const int b = __builtin_ctz(w);
+        w &= w - 1u;
+        if (pos < kPlanMaxItems) s_item[pos] = tid * 32 + b;
+        ++pos;
+      }
+      if (tid == 63) s_nact = incl;
+    }
+    __syncthreads();
+    static_assert(kPlanMaxItems <= kPlanGroupOffsets, "items of one group");
+    const int na = s_nact;
+    if (na > kPlanMaxItems ||
+        (na > 0 && s_item[0] / kPlanGroupOffsets != s_item[na - 1] / kPlanGroupOffsets)) {
+      // (uniform) the GEMM gathers this tile directly
+      if (tid == 0) count[tile] = kLdsRows;
+      return;
+    }
+  }
+  const int n_ent = kTileRows * (COMPACT ? s_nact : kv);
   // ---- entries into registers; window and items
   int32_t v[PER];
   int32_t lo = kNone, hi = -1;
@@ -72,13 +145,14 @@ __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
     const int e = i * kPlanThreads + tid;
     int32_t key = kNone;
     if (e < n_ent) {
-      const int k = e / kTileRows;
-      const int64_t r = r0 + (e - k * kTileRows);
-      if (r < M && ((live >> k) & 1u)) {
+      const int q = e / kTileRows;  // dense: the offset; COMPACT: the item
+      const int k = COMPACT ? s_item[q] : q;
+      const int64_t r = r0 + (e - q * kTileRows);
+      if (r < M && (COMPACT || ((s_live[k >> 5] >> (k & 31)) & 1u))) {
         const int32_t x = pairs[int64_t(k) * M + r];
         if (x >= 0 && x < n_src) {
           key = x;
-          s_item[k] = 0;  // every writer stores the same value
+          if (!COMPACT) s_item[k] = 0;  // every writer stores the same value
         }
       }
     }
@@ -157,9 +231,12 @@ __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
 #pragma unroll
     for (int i = 0; i < PER; ++i) keys[i * kPlanThreads + tid] = v[i];
     __syncthreads();
-    for (int size = 2; size <= NP; size <<= 1) {
+    // the entries past n_ent are kNone, already in place: sort the first np2
+    int np2 = 2 * kPlanThreads;
+    while (np2 < n_ent) np2 <<= 1;
+    for (int size = 2; size <= np2; size <<= 1) {
       for (int half = size >> 1; half > 0; half >>= 1) {
-        for (int i = tid; i < NP / 2; i += kPlanThreads) {
+        for (int i = tid; i < np2 / 2; i += kPlanThreads) {
           const int a = 2 * i - (i & (half - 1));
           const int c = a + half;
           const bool up = (a & size) == 0;
@@ -202,9 +279,11 @@ __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
   for (int i = U + tid; i < kLdsRows; i += kPlanThreads) rows_t[i] = -1;
 
   // items of the tile: the offsets with a pair among its rows, numbered in
-  // ascending order by one wave (kv <= kPlanMaxKv = 64 lanes)
-  static_assert(kPlanMaxKv <= 64, "one wave numbers the items");
-  if (tid < 64) {
+  // ascending order by one wave (dense: kv <= kPlanDenseKv <= 64 lanes)
+  if (COMPACT) {
+    if (tid < E) koff_out[tile * E + tid] = tid < s_nact ? s_item[tid] : -1;
+    if (tid == 0) nact_out[tile] = s_nact;
+  } else if (tid < 64) {
     int32_t* ko = koff_out + tile * E;
     const bool live = tid < kv && s_item[tid] == 0;
     const uint64_t m = __builtin_amdgcn_ballot_w64(live);
@@ -233,8 +312,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_build_kernel(
   for (int i = 0; i < PER; ++i) {
     const int e = i * kPlanThreads + tid;
     if (e >= n_ent) continue;
-    const int k = e / kTileRows, lr = e - k * kTileRows;
-    const int item = s_item[k];
+    const int q = e / kTileRows, lr = e - q * kTileRows;
+    const int item = COMPACT ? q : s_item[q];
     if (item < 0) continue;
     uint16_t a = zero;
     const int32_t x = v[i];
@@ -385,11 +464,11 @@ __global__ __launch_bounds__(256) void permute_table_kernel(const int32_t* __res
   }
 }
 
-template <int NP>
+template <int NP, bool COMPACT = false>
 static void launch_plan(unsigned nt, hipStream_t s, const int32_t* pairs, int64_t M, int kv,
                         int64_t n_src, const PlanLayout& p, char* b, const uint32_t* words,
                         int mic) {
-  plan_build_kernel<NP><<<nt, kPlanThreads, 0, s>>>(
+  plan_build_kernel<NP, COMPACT><<<nt, kPlanThreads, 0, s>>>(
       pairs, M, kv, n_src, reinterpret_cast<int32_t*>(b + p.count_off),
       reinterpret_cast<int32_t*>(b + p.rows_off), reinterpret_cast<int32_t*>(b + p.nact_off),
       reinterpret_cast<int32_t*>(b + p.koff_off), reinterpret_cast<uint16_t*>(b + p.addr_off),
@@ -431,7 +510,10 @@ int sp_gather_plan_build(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_
   const unsigned nt = unsigned(p.ntiles);
   const int n_ent = kTileRows * int(kv);
   const int k = int(kv);
-  if (n_ent <= 1024) launch_plan<1024>(nt, s, pairs, M, k, n_src, p, b, row_words, words_per_row);
+  if (kv > kPlanDenseKv)
+    launch_plan<kTileRows * kPlanMaxItems, true>(nt, s, pairs, M, k, n_src, p, b, row_words,
+                                                 words_per_row);
+  else if (n_ent <= 1024) launch_plan<1024>(nt, s, pairs, M, k, n_src, p, b, row_words, words_per_row);
   else if (n_ent <= 2048) launch_plan<2048>(nt, s, pairs, M, k, n_src, p, b, row_words, words_per_row);
   else if (n_ent <= 4096) launch_plan<4096>(nt, s, pairs, M, k, n_src, p, b, row_words, words_per_row);
   else if (n_ent <= 8192) launch_plan<8192>(nt, s, pairs, M, k, n_src, p, b, row_words, words_per_row);

@@ -218,7 +218,21 @@ SURE_PAIRS_PER_ROW = 1.05
 #: or off (False) for every ordered call ("auto": by that rule).
 THIN_MAX_ITEMS_PER_TILE = 1.5
 THIN_TILES = "auto"
-_PLAN_MAX_KV = 64  # kv range of the gather plans (sp_gather_plan_bytes)
+#: kv range of the gather plans (sp_gather_plan_bytes: 1..1024).  A plan tile
+#: holds at most 64 live offsets (more: its rows are gathered directly), so
+#: natural-order tables are planned up to kv = 64 only (a 5^3 window's natural
+#: tiles hold ~125 live offsets each); mask-ordered tables, whose tiles hold
+#: rows of like masks, up to 1024.
+_PLAN_MAX_KV = 64
+_ORDERED_PLAN_MAX_KV = 1024
+#: Above 64 offsets a plan tile also lists only items within one group of 64
+#: offsets (the direct kernel's summation groups); a mask-ordered plan with
+#: more than ORDERED_PLAN_MAX_OVERFLOW of its tiles gathered directly is
+#: dropped at the decision (one more read-back), as the direct kernel with the
+#: rows' mask words reads fewer table entries: the 4-D submanifold table of
+#: ~500k voxels (time neighbours at offsets 13, 40 and 67 in most tiles) had
+#: 1 899 of 1 960 tiles overflow, 289 us planned against 287 us direct.
+ORDERED_PLAN_MAX_OVERFLOW = 0.5
 _STATS_MAX_KV = 512  # kv range of sp_table_stats
 
 
@@ -302,9 +316,10 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool 
         # without the permuted table's gather plan as the call asks (built on
         # the first call that wants it)
         order, perm, plan = step
-        if not (plan_ok and kv <= _PLAN_MAX_KV):
+        if not (plan_ok and kv <= _ORDERED_PLAN_MAX_KV):
             return step if plan is None else (order, perm, None)
-        if plan is None and not torch.cuda.is_current_stream_capturing():
+        if (plan is None and not getattr(perm, "_spconv_triton_noplan", False)
+                and not torch.cuda.is_current_stream_capturing()):
             step = (order, perm, gather_plan(perm, n_src, getattr(perm, "_spconv_triton_words",
                                                                    None)))
             pairs._spconv_triton_order = (stamp, step)
@@ -317,7 +332,7 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool 
         pairs._spconv_triton_order = (stamp, "seen")
         return None
 
-    planned = plan_ok and kv <= _PLAN_MAX_KV
+    planned = plan_ok and kv <= _ORDERED_PLAN_MAX_KV
 
     def mfma_rows(stats):  # rows the GEMM multiplies: per live tile or wave offset
         return 256 * stats[1] if planned else 64 * stats[2]
@@ -334,8 +349,12 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool 
         masked = table_stats(perm, n_src) if not sure else None
         if sure or mfma_rows(masked) <= ORDER_MAX_WORK_RATIO * done:
             plan = gather_plan(perm, n_src, words) if planned else None
-            variant = (order, perm, plan)
             tiles = (M + 255) // 256
+            if (plan is not None and kv > _PLAN_MAX_KV
+                    and plan_overflow_count(plan) > ORDERED_PLAN_MAX_OVERFLOW * tiles):
+                plan = None
+                perm._spconv_triton_noplan = True
+            variant = (order, perm, plan)
             perm._spconv_triton_thin = (
                 (mode != "mask" and masked is None)  # about one pair per row
                 or (masked is not None and masked[1] <= THIN_MAX_ITEMS_PER_TILE * tiles))
@@ -425,7 +444,7 @@ def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: 
     if split:  # the GEMM's reduction dimension is tripled
         K, C = (3 * K, C) if transpose else (K, 3 * C)
     if variant is None:
-        plan = gather_plan(pairs, a.shape[0]) if use_plan else None
+        plan = gather_plan(pairs, a.shape[0]) if use_plan and kv <= _PLAN_MAX_KV else None
         if plan is not None:
             variant = key_order_variant(pairs, a.shape[0], plan)
     if variant is not None:

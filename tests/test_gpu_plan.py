@@ -24,6 +24,8 @@ DEV = "cuda:0"
 TILE = 256
 LDS_ROWS = 896  # kLdsRows of csrc/sp_plan.h
 GROUP = 4  # kItemGroup of csrc/sp_plan.h
+MAX_ITEMS = 64  # kPlanMaxItems of csrc/sp_plan.h: more live offsets make an overflow tile
+GROUP_OFFSETS = 64  # kPlanGroupOffsets: so do live offsets in two groups of 64
 
 
 def _align(v, a=256):
@@ -39,7 +41,7 @@ def _chunk_base(slot):
 def _parse(plan, kv, M):
     """Split a plan buffer into its parts (layout of csrc/sp_plan.h)."""
     nt = (max(M, 1) + TILE - 1) // TILE
-    E = (kv + GROUP - 1) // GROUP * GROUP
+    E = (min(kv, MAX_ITEMS) + GROUP - 1) // GROUP * GROUP
     buf = plan.cpu().numpy()
     count_off = 256
     ovf_off = _align(count_off + nt * 4)
@@ -61,15 +63,18 @@ def _parse(plan, kv, M):
     }
 
 
-def _check_plan(pf, n_src):
+def _check_plan(pf, n_src, words=None):
     """Every part of the plan against numpy: per tile np.unique of the valid
     sources, the offsets with a pair (ascending) then -1, and per (item, row)
     the staged address of the row's rank in the unique list (np.searchsorted),
-    or of the zero row U, up to the end of the tile's last group of items."""
+    or of the zero row U, up to the end of the tile's last group of items.  A
+    tile with more than MAX_ITEMS live offsets is an overflow tile whose count
+    reads LDS_ROWS, as does one whose live offsets span two groups of
+    GROUP_OFFSETS.  words: build the plan from the rows' mask words too."""
     from spconv_triton.pytorch._impl import gemm
 
     kv, M = pf.shape
-    plan = gemm.gather_plan(pf, n_src)
+    plan = gemm.gather_plan(pf, n_src, words)
     assert plan is not None
     n_over_host = gemm.plan_overflow_count(plan)
     P = _parse(plan, kv, M)
@@ -78,6 +83,12 @@ def _check_plan(pf, n_src):
     for t in range((M + TILE - 1) // TILE):
         blk = p[:, t * TILE:(t + 1) * TILE]
         valid = (blk >= 0) & (blk < n_src)
+        live = np.nonzero(valid.any(axis=1))[0]
+        if live.size > MAX_ITEMS or (live.size and live[0] // GROUP_OFFSETS
+                                      != live[-1] // GROUP_OFFSETS):
+            assert P["count"][t] == LDS_ROWS, f"tile {t}: {live} items, not an overflow tile"
+            overflow.append(t)
+            continue
         uniq = np.unique(blk[valid])
         U = uniq.size
         assert P["count"][t] == U, f"tile {t}: count {P['count'][t]} != {U}"
@@ -88,7 +99,6 @@ def _check_plan(pf, n_src):
         assert (P["rows"][t, U:] == -1).all()
         addr = np.where(valid, _chunk_base(np.searchsorted(uniq, np.where(valid, blk, 0))),
                         _chunk_base(U))
-        live = np.nonzero(valid.any(axis=1))[0]
         n = live.size
         assert P["nact"][t] == n, f"tile {t}: {P['nact'][t]} items != {n}"
         np.testing.assert_array_equal(P["koff"][t, :n], live)
@@ -114,7 +124,9 @@ def test_plan_layout_limits():
 
     L = _lib.lib()
     assert L.sp_gather_plan_bytes(1000, 64) > 0
-    assert L.sp_gather_plan_bytes(1000, 65) == 0  # kv above the planned kernel's range
+    # above 64 offsets a tile lists at most 64 items: the same size as kv = 64
+    assert L.sp_gather_plan_bytes(1000, 1024) == L.sp_gather_plan_bytes(1000, 64)
+    assert L.sp_gather_plan_bytes(1000, 1025) == 0  # kv above the planned kernel's range
     assert L.sp_gather_plan_bytes(1000, 0) == 0
 
 
@@ -156,7 +168,7 @@ def test_plan_matches_numpy(case):
         assert n_over == 0
 
 
-@pytest.mark.parametrize("kv", [27, 64])
+@pytest.mark.parametrize("kv", [27, 64, 81, 125])
 def test_plan_with_row_words_identical(kv):
     """A plan built with the rows' mask words (the build reads only the offsets
     some row of a tile has) equals the plan built from the table alone in
@@ -173,11 +185,12 @@ def test_plan_with_row_words_identical(kv):
         perm = gemm.permute_table(pf, order, words if kv <= 32 else None)
         A = _parse(gemm.gather_plan(perm.clone(), 20_000), kv, M)
         B = _parse(gemm.gather_plan(perm, 20_000, words), kv, M)
-        for key in ("count", "ovf", "nact"):
+        for key in ("count", "ovf"):
             np.testing.assert_array_equal(A[key], B[key], f"{key}, p_valid={p_valid}")
         for t in range(A["count"].shape[0]):
             if A["count"][t] >= LDS_ROWS:
-                continue
+                continue  # an overflow tile: nothing else is written for it
+            assert A["nact"][t] == B["nact"][t], f"tile {t} items, p_valid={p_valid}"
             n = int(A["nact"][t])
             n4 = (n + GROUP - 1) // GROUP * GROUP
             np.testing.assert_array_equal(A["rows"][t], B["rows"][t])
@@ -264,6 +277,108 @@ def test_planned_overflow_tiles(dtype):
     assert torch.equal(planned, direct)
 
 
+@pytest.mark.parametrize("kv", [81, 125, 343])
+def test_plan_many_offsets(kv):
+    """kv above 64: the build finds a tile's live offsets first (by a scan of
+    its entries, or from the rows' mask words) and lists only those, at most
+    64; tiles with more are overflow tiles.  The table: every row pairs at
+    the centre offset, ~0.3 other pairs per row, and rows 0..299 pair at half
+    of all offsets within 700 sources (their tiles: too many offsets, but few
+    distinct rows).  Checked against numpy in natural order and in mask order
+    (tiles of like masks: most hold one or two offsets, the tiles of rows
+    0..299 overflow), the latter built both ways."""
+    from spconv_triton.pytorch._impl import gemm
+
+    rng = np.random.default_rng(kv)
+    M, n_src = 3000, 4000
+    t = rng.integers(0, n_src, size=(kv, M)).astype(np.int32)
+    t[rng.random((kv, M)) > 0.3 / kv] = -1
+    t[kv // 2] = rng.permutation(n_src)[:M]
+    t[:, :300] = np.where(rng.random((kv, 300)) < 0.5, t[kv // 2, :300] % 700, -1)
+    t[kv // 2, :300] = rng.integers(0, 700, 300)
+    pf = torch.from_numpy(t).to(DEV)
+    tiles = (M + TILE - 1) // TILE
+    assert _check_plan(pf.clone(), n_src) >= 2  # (rows 0..299)
+    order, words = gemm.mask_order(pf, with_words=True)
+    perm = gemm.permute_table(pf, order)
+    n_a = _check_plan(perm.clone(), n_src)
+    n_b = _check_plan(perm.clone(), n_src, words)
+    assert n_a == n_b and 1 <= n_a < tiles
+
+
+def _planned_vs_direct(a, w, pairs, M, plan, dtype):
+    """The direct kernel (no plan) and the planned kernels (staged, thin) over
+    a table in its own row order, through the C ABI: [direct, staged, thin]."""
+    from spconv_triton.pytorch._impl import _lib, gemm
+
+    L = _lib.lib()
+    K, kv, C = w.shape[0], pairs.shape[0], w.shape[-1]
+    packed = gemm.packed_weight(w, None, dtype, False)
+    dt = _lib.dtype_code(dtype)
+    s = _lib.stream_of(a.device)
+    ident = torch.arange(M, dtype=torch.int32, device=DEV)
+    outs = []
+    for mode in ("direct", "staged", "thin"):
+        out = torch.full((M, K), float("nan"), dtype=dtype, device=DEV)
+        if mode == "direct":
+            rc = L.sp_conv_gemm_packed(_lib.ptr(a), dt, a.shape[0], _lib.ptr(packed), K, kv, C, 0,
+                                       0, _lib.ptr(pairs), M, None, None, _lib.ptr(out), dt, s)
+        else:
+            rc = L.sp_conv_gemm_ordered(_lib.ptr(a), dt, a.shape[0], _lib.ptr(packed), K, kv, C,
+                                        0, 0, _lib.ptr(pairs), M, _lib.ptr(ident),
+                                        _lib.ptr(plan), plan.numel(), int(mode == "thin"), None,
+                                        0, _lib.ptr(out), dt, s)
+        _lib.check(rc, mode)
+        outs.append(out)
+    torch.cuda.synchronize()
+    return outs
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_planned_tiles_within_one_offset_group(dtype):
+    """kv = 81: the direct kernel sums a row's offsets 64 at a time, each group
+    over all reduction chunks, the planned kernels a tile's items chunk by
+    chunk.  The plan therefore lists only tiles whose items lie in one group
+    of 64 offsets; a tile with items in both ({13, 40, 67}, as the time
+    neighbours of a 4-D submanifold table; {63, 64}; 22 items) or with more
+    than 64 items is an overflow tile, gathered directly.  Tiles in group 0
+    ({13, 40}; 32 items) and group 1 ({64}; {70, 80}; 11 items) are staged or
+    thin, plus one item only and one tile with no pair; each tile's sources
+    lie in a window of 250 rows.  C = 96 spans several chunks in every dtype.
+    The staged and the thin kernel (12 workgroups: its quarter instance)
+    equal the direct kernel bit for bit."""
+    from spconv_triton.pytorch._impl import gemm
+
+    rng = np.random.default_rng(5)
+    kv, n_src, C, K = 81, 3000, 96, 64
+    sets = [[13, 40, 67], [13, 40], [63, 64], [64], list(range(1, 12)) + list(range(65, 76)),
+            list(range(0, 64, 2)), list(range(70)), [70, 80], [], list(range(65, 76)), [40],
+            [13, 40, 67]]
+    spans = {0, 2, 4, 6, 11}
+    M = TILE * len(sets) - 77  # a partial last tile
+    t = np.full((kv, TILE * len(sets)), -1, dtype=np.int32)
+    for ti, ks in enumerate(sets):
+        for k in ks:
+            live = rng.random(TILE) < 0.7
+            # sources in a window of 250 rows: the tile's rows fit the thin layout
+            src = ti * 200 + rng.integers(0, 250, TILE)
+            t[k, ti * TILE:(ti + 1) * TILE] = np.where(live, src, -1)
+    t[:, M:] = -1
+    pf = torch.from_numpy(np.ascontiguousarray(t[:, :M])).to(DEV)
+    assert _check_plan(pf.clone(), n_src) == len(spans)
+    P = _parse(gemm.gather_plan(pf, n_src), kv, M)
+    for ti in range(len(sets)):
+        assert (P["count"][ti] == LDS_ROWS) == (ti in spans), f"tile {ti}"
+    torch.manual_seed(7)
+    x, _ = _q(torch.randn(n_src, C), dtype)
+    w, _ = _q(torch.randn(K, kv, C) / np.sqrt(kv * C), dtype)
+    plan = gemm.gather_plan(pf, n_src)
+    direct, staged, thin = _planned_vs_direct(x, w, pf, M, plan, dtype)
+    assert not torch.isnan(direct).any()
+    assert torch.equal(staged, direct), "staged kernel differs from the direct kernel"
+    assert torch.equal(thin, direct), "thin kernel differs from the direct kernel"
+
+
 def test_planned_metric_shape():
     """The benchmark layer's shape: 200k-voxel surface cloud, 64 -> 64, fp16."""
     from bench_data import surface_cloud
@@ -333,8 +448,8 @@ def _orders(a, w, bias, transpose, pairs, M):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("case", ["subm", "strided", "kv125", "sparse_wide", "transposed",
-                                  "subm_long"])
+@pytest.mark.parametrize("case", ["subm", "strided", "kv125", "kv125_chunks", "sparse_wide",
+                                  "transposed", "subm_long"])
 def test_mask_row_order_bit_identical(case, dtype):
     """Every row sums its offsets in ascending order whatever tile it falls in,
     so the mask-ordered GEMM (staged, overflow and direct tiles, and the thin
@@ -342,7 +457,9 @@ def test_mask_row_order_bit_identical(case, dtype):
     equals the natural-order one bit for bit, forward and input gradient.
     subm_long: a forward grid of 1 175 workgroups (5 column blocks), where the
     16-bit thin kernel gives its direct tiles to direct_tile, and a dgrad grid
-    of 235, where it splits them into quarters."""
+    of 235, where it splits them into quarters.  kv125_chunks: 125 offsets
+    (two of the direct kernel's groups of 64) over several reduction chunks,
+    where only tiles whose items lie in one group are planned."""
     from spconv_triton.pytorch._impl import gemm
 
     rng = np.random.default_rng(44)
@@ -354,6 +471,8 @@ def test_mask_row_order_bit_identical(case, dtype):
         grid, n, stride = 28, 5000, 2
     elif case == "kv125":
         grid, n, stride, ks = 20, 2500, 1, 5
+    elif case == "kv125_chunks":
+        grid, n, stride, ks, C, K = 40, 2000, 1, 5, 96, 64
     elif case == "subm_long":
         grid, n, stride, C, K = 48, 60000, 1, 32, 320
     elif case == "transposed":  # about one pair per output: thin tiles; 2 column blocks
@@ -385,6 +504,10 @@ def test_mask_row_order_bit_identical(case, dtype):
     if case == "transposed":
         P = int((pf >= 0).sum())
         assert P <= 1.1 * pf.shape[1], "the case must have about one pair per row"
+    if case == "kv125_chunks":
+        plan = getattr(pf, "_spconv_triton_order")[1][2]
+        assert gemm.plan_overflow_count(plan) < (pf.shape[1] + 255) // 256, \
+            "the case must plan some tiles"
     if case == "sparse_wide":
         variant = getattr(pf, "_spconv_triton_order")[1]
         plan = variant[2]
