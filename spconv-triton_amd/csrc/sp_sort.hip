@@ -412,13 +412,20 @@ __global__ void mask_gather(const uint32_t* __restrict__ words, const uint32_t* 
 }
 
 // ---- sort of single-word masks ------------------------------------------------
-// The mask sort of tables with kv <= 32 (one word per row) and at most
-// kRsFusedTiles tiles: the items are (key, row) pairs carried from pass to
-// pass, so no pass gathers the words through a permutation, and the last
-// pass writes pair_mask and argsort itself (no separate gather).  (Adding the
-// next pass's histogram into global memory from each scatter with atomics, to
-// save the histogram launches, measured slower: 27 us per scatter instead of
-// 14, the cross-XCD atomics costing more than the launches they save.)
+// The mask sort of tables with kv <= 32 (one word per row): the items are
+// (key, row) pairs carried from pass to pass, so no pass gathers the words
+// through a permutation, and the last pass writes pair_mask and argsort itself
+// (no separate gather).  A pass is three launches: the tiles' histograms,
+// stored digit-major; rs_digit_prefix (one workgroup per digit: the digit's
+// exclusive prefix over the tiles, in place, and its total); the scatter, whose
+// workgroups read their own 512 prefixes and the 512 totals.  (Measured on the
+// 200k-row metric table, 3 passes: with tile-major histograms summed by every
+// scatter workgroup itself, two launches a pass, each scatter took 15 us
+// instead of 7.4 and the sort 63 us instead of 55: 98 workgroups each reading
+// all 98 tiles' histograms cost more than a launch.  Adding the next pass's
+// histogram into global memory from each scatter with atomics, to save the
+// histogram launches, measured slower still: 27 us per scatter, the cross-XCD
+// atomics costing more than the launches they save.)
 constexpr int kMsMaxPasses = 4;
 
 template <bool kFirst>
@@ -426,7 +433,7 @@ __global__ __launch_bounds__(kRsThreads) void ms_hist(const uint32_t* __restrict
                                                      uint32_t split,
                                                      const uint32_t* __restrict__ keys_in,
                                                      int64_t n, int shift, int db,
-                                                     uint32_t* __restrict__ hist) {
+                                                     uint32_t* __restrict__ hist, int64_t ntiles) {
   __shared__ uint32_t cnt[kRsMaxRadix];
   for (int i = threadIdx.x; i < kRsMaxRadix; i += kRsThreads) cnt[i] = 0;
   __syncthreads();
@@ -449,7 +456,7 @@ __global__ __launch_bounds__(kRsThreads) void ms_hist(const uint32_t* __restrict
   }
   __syncthreads();
   for (int i = threadIdx.x; i < kRsMaxRadix; i += kRsThreads)
-    hist[int64_t(blockIdx.x) * kRsMaxRadix + i] = cnt[i];  // [tile][digit], row pitch 512
+    hist[int64_t(i) * ntiles + blockIdx.x] = cnt[i];  // [digit][tile]
 }
 
 template <bool kFirst, bool kLast>
@@ -457,7 +464,8 @@ __global__ __launch_bounds__(kRsThreads) void ms_scatter(
     const uint32_t* __restrict__ words, uint32_t split, const uint32_t* __restrict__ keys_in,
     const uint32_t* __restrict__ rows_in, uint32_t* __restrict__ keys_out,
     uint32_t* __restrict__ rows_out, int32_t* __restrict__ pm_out, int32_t* __restrict__ ar_out,
-    int64_t n, int shift, int db, const uint32_t* __restrict__ hist, int64_t ntiles) {
+    int64_t n, int shift, int db, const uint32_t* __restrict__ hist,
+    const uint32_t* __restrict__ totals, int64_t ntiles) {
   __shared__ __align__(16) uint16_t seg[kRsSegs][kRsMaxRadix];
   __shared__ uint32_t tile_base[kRsMaxRadix];
   __shared__ uint32_t scan_lds[kRsThreads / 64 + 1];
@@ -483,7 +491,14 @@ __global__ __launch_bounds__(kRsThreads) void ms_scatter(
   for (int r = 0; r < kRsRounds; ++r) digits[r] = (keys[r] >> shift) & dmask;
   // (the barriers of its block scan also order the zeroing of seg before
   // the segment counts below)
-  fused_tile_base(hist, ntiles, kRsMaxRadix, tile_base, scan_lds);
+  {
+    const int d = int(threadIdx.x);
+    const uint32_t t = totals[d];
+    const uint32_t pre = hist[int64_t(d) * ntiles + blockIdx.x];
+    uint32_t all = 0;
+    const uint32_t below = block_exclusive_scan<kRsThreads>(t, scan_lds, &all);
+    tile_base[d] = below + pre;
+  }
 #pragma unroll
   for (int r = 0; r < kRsRounds; ++r) {
     const int64_t idx = base + r * kRsThreads + wave * 64 + lane;
@@ -531,6 +546,7 @@ template <class W>
 static void mask_fused_layout(W& w, int64_t n) {
   for (int i = 0; i < 4; ++i) w.template take<uint32_t>(size_t(n));  // keys/rows ping-pong
   w.template take<uint32_t>(size_t(kRsMaxRadix) * size_t(cdiv(n, kRsTile)));  // tile histograms
+  w.template take<uint32_t>(size_t(kRsMaxRadix));  // digit totals
 }
 
 static size_t mask_fused_ws_bytes(int64_t n) {
@@ -539,8 +555,8 @@ static size_t mask_fused_ws_bytes(int64_t n) {
   return z.off;
 }
 
-// Whether sp_mask_sort takes this path (single words, <= kRsFusedTiles tiles).
-static bool mask_fused_ok(int64_t n, int mic) { return mic == 1 && cdiv(n, kRsTile) <= kRsFusedTiles; }
+// Whether sp_mask_sort takes this path (single words).
+static bool mask_fused_ok(int64_t n, int mic) { return mic == 1 && cdiv(n, kRsTile) <= kMaxGridX; }
 
 static int sort_masks_fused(const uint32_t* words, int64_t n, int kv, uint32_t split,
                             int32_t* pm, int32_t* ar, void* ws, hipStream_t s) {
@@ -551,6 +567,7 @@ static int sort_masks_fused(const uint32_t* words, int64_t n, int kv, uint32_t s
   uint32_t* rb = c.take<uint32_t>(size_t(n));
   const int64_t ntiles = cdiv(n, kRsTile);
   uint32_t* hist = c.take<uint32_t>(size_t(kRsMaxRadix) * size_t(ntiles));
+  uint32_t* totals = c.take<uint32_t>(size_t(kRsMaxRadix));
   int bits = kv;
   const int top = split ? 32 - __builtin_clz(split) : 0;
   bits = bits < top ? bits : top;
@@ -570,14 +587,17 @@ static int sort_masks_fused(const uint32_t* words, int64_t n, int kv, uint32_t s
   for (int p = 0; p < passes; ++p) {
     const bool first = p == 0, last = p + 1 == passes;
     if (first)
-      ms_hist<true><<<grid, block, 0, s>>>(words, split, nullptr, n, shift, widths[p], hist);
+      ms_hist<true><<<grid, block, 0, s>>>(words, split, nullptr, n, shift, widths[p], hist,
+                                           ntiles);
     else
-      ms_hist<false><<<grid, block, 0, s>>>(nullptr, 0u, kin, n, shift, widths[p], hist);
+      ms_hist<false><<<grid, block, 0, s>>>(nullptr, 0u, kin, n, shift, widths[p], hist, ntiles);
+    SP_LAUNCHED();
+    rs_digit_prefix<<<dim3(unsigned(kRsMaxRadix)), dim3(kDsThreads), 0, s>>>(hist, ntiles, totals);
     SP_LAUNCHED();
     auto kern = first ? (last ? ms_scatter<true, true> : ms_scatter<true, false>)
                       : (last ? ms_scatter<false, true> : ms_scatter<false, false>);
     kern<<<grid, block, 0, s>>>(words, split, kin, rin, kout, rout, pm, ar, n, shift, widths[p],
-                                hist, ntiles);
+                                hist, totals, ntiles);
     SP_LAUNCHED();
     shift += widths[p];
     kin = kout;

@@ -391,8 +391,7 @@ def test_large_subm_properties():
 @pytest.mark.parametrize("n,grid", [(200_000, 256), (600_000, 512)])
 def test_mask_sort_stable_large(n, grid):
     """The mask sort is a stable ascending sort of the mask words: at 200k rows
-    (98 radix tiles, placements summed inside the scatter) and 600k rows (293
-    tiles, device-wide scan of the histograms), mask_argsort equals numpy's
+    (98 radix tiles) and 600k rows (293 tiles), mask_argsort equals numpy's
     stable argsort of the words that the table's bits define."""
     from spconv_triton.core import ConvAlgo
     from spconv_triton.pytorch import ops
@@ -428,24 +427,25 @@ def _expect_sorted(w_np, split):
     return order.astype(np.int64), keys[order].astype(np.int64)
 
 
-def test_mask_sort_single_launch_cases():
-    """Single-word mask sorts of up to 128 radix tiles run as one launch whose
-    tiles meet at device-wide barriers.  Against numpy's stable argsort: one
-    to 128 tiles (partial last tiles, a single row), 1 to 4 passes (kv 5, 9,
-    27, 32), a split mask, heavily repeated keys; every sort reuses one
-    workspace that starts as random bytes, so barrier flags left by the
-    previous sort (and garbage) sit in the buffer and must not be taken for the
-    current sort's."""
+def test_mask_sort_single_word_cases():
+    """Single-word mask sorts carry (key, row) pairs from pass to pass, with
+    digit-major tile histograms and a per-digit prefix launch.  Against numpy's
+    stable argsort: one to 160 radix tiles of 2048 rows (partial last tiles, a
+    single row), 1 to 4 passes (kv 5, 9, 27, 32), a split mask, heavily
+    repeated keys; every sort reuses one workspace that starts as random bytes
+    (and holds the previous sort's histograms), so nothing may depend on its
+    contents."""
     from spconv_triton.pytorch._impl import _lib
 
     rng = np.random.default_rng(5)
     L = _lib.lib()
-    n_max = 128 * 2048
+    n_max = 160 * 2048
     ws = torch.from_numpy(rng.integers(0, 256, size=L.sp_mask_sort_workspace_size(n_max, 1),
                                        dtype=np.uint8)).to(DEV)
     cases = [(1, 27, 0xFFFFFFFF), (100, 9, 0xFFFFFFFF), (2048, 27, 0xFFFFFFFF),
              (2049, 5, 0xFFFFFFFF), (5000, 32, 0xFFFFFFFF), (70_001, 27, 0x3FFF),
-             (131_072, 18, 0xFFFFFFFF), (n_max - 3, 27, 0xFFFFFFFF), (n_max, 32, 0xFFFF0000)]
+             (131_072, 18, 0xFFFFFFFF), (128 * 2048 + 1, 27, 0xFFFFFFFF),
+             (n_max - 3, 27, 0xFFFFFFFF), (n_max, 32, 0xFFFF0000)]
     for n, kv, split in cases:
         hi = (1 << kv) - 1
         w_np = rng.integers(0, hi + 1, size=n, dtype=np.int64)
@@ -458,14 +458,13 @@ def test_mask_sort_single_launch_cases():
         np.testing.assert_array_equal(ar.cpu().numpy(), order, f"argsort n={n} kv={kv}")
         np.testing.assert_array_equal(pm.cpu().numpy().astype(np.int64) & 0xFFFFFFFF, keys,
                                       f"sorted words n={n} kv={kv}")
-    assert _sort_drops() == 0, "a sort scatter dropped positions or a barrier timed out"
+    assert _sort_drops() == 0, "a sort scatter dropped positions"
 
 
 def test_mask_sort_graph_replays():
-    """The single-launch mask sort captured into a HIP graph: every replay (new
+    """The single-word mask sort captured into a HIP graph: every replay (new
     words copied in between, eager sorts on the same workspace between replays)
-    equals numpy's stable argsort -- each launch, replays included, takes a new
-    barrier epoch."""
+    equals numpy's stable argsort."""
     from spconv_triton.pytorch._impl import _lib
 
     rng = np.random.default_rng(9)

@@ -506,8 +506,11 @@ def test_mask_row_order_bit_identical(case, dtype):
         assert P <= 1.1 * pf.shape[1], "the case must have about one pair per row"
     if case == "kv125_chunks":
         plan = getattr(pf, "_spconv_triton_order")[1][2]
-        assert gemm.plan_overflow_count(plan) < (pf.shape[1] + 255) // 256, \
-            "the case must plan some tiles"
+        # a mask-ordered kv > 64 plan is kept only while at most half its tiles
+        # overflow (here most tiles hold offsets of both groups of 64)
+        tiles = (pf.shape[1] + 255) // 256
+        assert plan is None or gemm.plan_overflow_count(plan) <= \
+            gemm.ORDERED_PLAN_MAX_OVERFLOW * tiles
     if case == "sparse_wide":
         variant = getattr(pf, "_spconv_triton_order")[1]
         plan = variant[2]
