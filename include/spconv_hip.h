@@ -240,6 +240,11 @@ size_t sp_gather_plan_bytes(int64_t M, int64_t kv);
 int sp_gather_plan_build(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_src,
                          const uint32_t* row_words, int32_t words_per_row, void* plan,
                          size_t plan_bytes, int64_t* n_overflow, void* stream);
+/* The number of overflow tiles of a built plan (same kv and M as its build),
+ * for callers that choose a row order by it; one kernel launch and one stream
+ * synchronization.  No reference entry point corresponds to it. */
+int sp_gather_plan_overflow(void* plan, size_t plan_bytes, int64_t kv, int64_t M,
+                            int64_t* n_overflow, void* stream);
 
 /* sp_conv_gemm_packed with a gather plan of `pairs` (built for the same kv, M
  * and n_src); no mask tables.  One kernel launch.  Results are bit-identical

@@ -19,7 +19,9 @@
 //
 // Layout of one plan buffer (256-byte aligned parts), E = min(kv, kPlanMaxItems)
 // rounded up to a multiple of kItemGroup:
-//   n_overflow                  int32   number of overflow tiles (below)
+//   n_overflow                  int32   number of overflow tiles (below); it and
+//                                       the overflow list are written only when
+//                                       asked for (sp_gather_plan_overflow)
 //   count[ntiles]               int32   U of the tile; U >= kLdsRows marks an
 //                                       overflow tile, whose rows do not fit in
 //                                       LDS or whose items are more than

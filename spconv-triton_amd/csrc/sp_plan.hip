@@ -19,12 +19,12 @@
 // first (from the rows' mask words, or by a scan of the tile's entries that
 // keeps only one bit per offset), numbered as items, and only their entries
 // are read: at most kPlanMaxItems of them, in one group of kPlanGroupOffsets,
-// a tile with more or spanning two groups being an overflow tile.  A second,
-// single-workgroup kernel lists the tiles whose rows do not fit in LDS; their
-// number is copied back to the host (the build's one synchronisation), so
-// that a GEMM launches the direct-gather kernel for them only when there are
-// any.  The plan depends only on the table, so the caller builds it once per
-// table and reuses it for every GEMM on that table.
+// a tile with more or spanning two groups being an overflow tile.  The GEMM
+// finds a plan's overflow tiles from their counts; on request only (the host's
+// row-order decisions), a second, single-workgroup kernel lists them and their
+// number is copied back (one synchronisation).  The plan depends only on the
+// table, so the caller builds it once per table and reuses it for every GEMM
+// on that table.
 #include "sp_plan.h"
 
 namespace sp {
@@ -475,6 +475,19 @@ static void launch_plan(unsigned nt, hipStream_t s, const int32_t* pairs, int64_
       p.E, words, mic);
 }
 
+// The overflow list and its count of a built plan (the build leaves them out
+// unless asked: no GEMM reads them), copied back to the host (one sync).
+static int list_overflow(const PlanLayout& p, const int32_t* count, int32_t* n_ovf,
+                         int32_t* ovf, int64_t* n_overflow, hipStream_t s) {
+  plan_overflow_kernel<<<1, kOvThreads, 0, s>>>(count, p.ntiles, n_ovf, ovf);
+  SP_LAUNCHED();
+  int32_t h = 0;
+  SP_HIP(hipMemcpyAsync(&h, n_ovf, sizeof(h), hipMemcpyDeviceToHost, s));
+  SP_HIP(hipStreamSynchronize(s));
+  *n_overflow = h;
+  return SP_OK;
+}
+
 }  // namespace sp
 
 using namespace sp;
@@ -519,15 +532,26 @@ int sp_gather_plan_build(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_
   else if (n_ent <= 8192) launch_plan<8192>(nt, s, pairs, M, k, n_src, p, b, row_words, words_per_row);
   else launch_plan<16384>(nt, s, pairs, M, k, n_src, p, b, row_words, words_per_row);
   SP_LAUNCHED();
-  plan_overflow_kernel<<<1, kOvThreads, 0, s>>>(count, p.ntiles, n_ovf, ovf);
-  SP_LAUNCHED();
-  if (n_overflow) {  // the count is only reported on request (it costs a sync)
-    int32_t h = 0;
-    SP_HIP(hipMemcpyAsync(&h, n_ovf, sizeof(h), hipMemcpyDeviceToHost, s));
-    SP_HIP(hipStreamSynchronize(s));
-    *n_overflow = h;
-  }
+  if (n_overflow) return list_overflow(p, count, n_ovf, ovf, n_overflow, s);
   return SP_OK;
+}
+
+int sp_gather_plan_overflow(void* plan, size_t plan_bytes, int64_t kv, int64_t M,
+                            int64_t* n_overflow, void* stream) {
+  SP_CHECK_ARG(n_overflow, "gather plan overflow: null count");
+  *n_overflow = 0;
+  SP_CHECK_ARG(kv >= 1 && kv <= kPlanMaxKv && M >= 0 && M < (int64_t(1) << 31),
+               "gather plan overflow: bad sizes kv=%lld M=%lld", (long long)kv, (long long)M);
+  if (M == 0) return SP_OK;
+  SP_CHECK_ARG(plan, "gather plan overflow: null plan");
+  const PlanLayout p = plan_layout(M, kv);
+  if (plan_bytes < p.total)
+    return set_error(SP_ERR_WORKSPACE, "gather plan overflow: buffer %zu < %zu", plan_bytes,
+                     p.total);
+  char* b = static_cast<char*>(plan);
+  return list_overflow(p, reinterpret_cast<const int32_t*>(b + p.count_off),
+                       reinterpret_cast<int32_t*>(b), reinterpret_cast<int32_t*>(b + p.overflow_off),
+                       n_overflow, as_stream(stream));
 }
 
 int sp_table_stats(const int32_t* pairs, int64_t kv, int64_t M, int64_t n_src, int64_t* stats,

@@ -112,6 +112,7 @@ _SIGNATURES = {
     "sp_conv_gemm_packed": (ctypes.c_int, [_P, _I32, _I64, _P, _I64, _I64, _I64, _I32, _I32, _P,
                                            _I64, _P, _P, _P, _I32, _P]),
     "sp_gather_plan_bytes": (_SZ, [_I64, _I64]),
+    "sp_gather_plan_overflow": (ctypes.c_int, [_P, _SZ, _I64, _I64, _P, _P]),
     "sp_gather_plan_build": (ctypes.c_int, [_P, _I64, _I64, _I64, _P, _I32, _P, _SZ,
                                             ctypes.POINTER(_I64), _P]),
     "sp_conv_gemm_planned": (ctypes.c_int, [_P, _I32, _I64, _P, _I64, _I64, _I64, _I32, _I32, _P,

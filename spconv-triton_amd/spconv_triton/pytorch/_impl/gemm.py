@@ -166,6 +166,7 @@ def gather_plan(pairs: torch.Tensor, n_src: int, words: torch.Tensor | None = No
     if nbytes == 0:
         return None
     plan = torch.empty(nbytes, dtype=torch.uint8, device=pairs.device)
+    plan._spconv_triton_dims = (kv, M)
     _lib.check(L.sp_gather_plan_build(_lib.ptr(pairs), kv, M, int(n_src), _lib.ptr(words),
                                       0 if words is None else words.shape[1], _lib.ptr(plan),
                                       nbytes, None, _lib.stream_of(pairs.device)),
@@ -425,9 +426,19 @@ def key_order_variant(pairs: torch.Tensor, n_src: int, plan: torch.Tensor):
 
 
 def plan_overflow_count(plan: torch.Tensor) -> int:
-    """Number of tiles of a plan whose distinct rows do not fit in LDS (the
-    plan's first int32; reading it synchronizes)."""
-    return int(plan[:4].view(torch.int32)[0].item())
+    """Number of tiles of a plan (from gather_plan) that the GEMM gathers
+    directly (``sp_gather_plan_overflow``: also writes the plan's overflow list;
+    synchronizes).  Memoised on the plan tensor, which never changes."""
+    n = getattr(plan, "_spconv_triton_novf", None)
+    if n is None:
+        kv, M = plan._spconv_triton_dims
+        out = ctypes.c_int64(0)
+        _lib.check(_lib.lib().sp_gather_plan_overflow(_lib.ptr(plan), plan.numel(), kv, M,
+                                                      ctypes.byref(out),
+                                                      _lib.stream_of(plan.device)),
+                   "sp_gather_plan_overflow")
+        n = plan._spconv_triton_novf = int(out.value)
+    return n
 
 
 def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: torch.Tensor,

@@ -39,7 +39,11 @@ def _chunk_base(slot):
 
 
 def _parse(plan, kv, M):
-    """Split a plan buffer into its parts (layout of csrc/sp_plan.h)."""
+    """Split a plan buffer into its parts (layout of csrc/sp_plan.h).  The
+    overflow count and list are written on request only: ask for them first."""
+    from spconv_triton.pytorch._impl import gemm
+
+    gemm.plan_overflow_count(plan)
     nt = (max(M, 1) + TILE - 1) // TILE
     E = (min(kv, MAX_ITEMS) + GROUP - 1) // GROUP * GROUP
     buf = plan.cpu().numpy()
