@@ -32,6 +32,31 @@ namespace sp {
 // ---------------------------------------------------------------------------
 // geometry
 // ---------------------------------------------------------------------------
+// Division of n < 2^31 by a fixed divisor 1 <= d < 2^31 as a multiply-high
+// and a shift (Granlund and Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994): with l = ceil(log2 d) and m = ceil(2^(31+l) / d),
+// floor(n * m / 2^(31+l)) = floor(n / d) for every n < 2^31, because
+// m * d - 2^(31+l) < d <= 2^l keeps the error term n * (m * d - 2^(31+l)) /
+// 2^(31+l) below 1 - (n mod d) / d.  For d >= 2, d > 2^(l-1) gives m < 2^32,
+// so the quotient is umulhi(n, m) >> (l - 1); d = 1 is the identity (m = 0
+// marks it).  The int32-key paths divide only such values (strides, output
+// extents): two instructions instead of a 32-bit division routine.
+struct Div31 {
+  uint32_t m;  // 0: d = 1
+  int sh;
+};
+
+static Div31 make_div31(uint32_t d) {
+  if (d <= 1) return Div31{0u, 0};
+  int l = 0;
+  while ((uint64_t(1) << l) < d) ++l;
+  return Div31{uint32_t(((uint64_t(1) << (31 + l)) + d - 1) / d), l - 1};
+}
+
+__device__ __forceinline__ uint32_t div31(uint32_t n, const Div31& q) {
+  return q.m ? (__umulhi(n, q.m) >> q.sh) : n;
+}
+
 struct GeomDev {
   int ndim;
   int mode;
@@ -40,6 +65,7 @@ struct GeomDev {
   int64_t in_shape[4];
   int64_t out_shape[4];
   int32_t ks[4], st[4], pad[4], dil[4];
+  Div31 st_div[4], out_div[4];  // for values below 2^31 (int32-key paths)
 };
 
 static int64_t prod_shape(const int64_t* s, int ndim) {
@@ -77,6 +103,8 @@ static int make_geom(const sp_geom* g, GeomDev* out) {
       d.st[i] = g->stride[i];
     }
     kv *= g->ksize[i];
+    d.st_div[i] = make_div31(uint32_t(d.st[i]));
+    d.out_div[i] = make_div31(uint32_t(d.out_shape[i] < (int64_t(1) << 31) ? d.out_shape[i] : 1));
   }
   SP_CHECK_ARG(kv <= 4096, "kernel volume %lld too large", (long long)kv);
   d.kv = int(kv);
@@ -149,7 +177,11 @@ __device__ __forceinline__ bool candidate_key(const GeomDev& g, const Coord& c, 
           o = num;
         } else {
           const U st = U(g.st[d]);
-          const U q = U(num >= 0 ? num : 0) / st;
+          U q;
+          if constexpr (sizeof(I) == 4)  // num < 2^31: the multiply-shift division
+            q = U(div31(uint32_t(num >= 0 ? num : 0), g.st_div[d]));
+          else
+            q = U(num >= 0 ? num : 0) / st;
           ok = ok && num >= 0 && U(num) == q * st;
           o = num >= 0 ? I(q) : I(-1);
         }
@@ -1183,14 +1215,24 @@ __global__ __launch_bounds__(256) void emit_bitmap_keys(const uint32_t* __restri
       const int b = __ffs(m) - 1;
       m &= m - 1u;
       uint32_t rem = uint32_t(w) * 32u + uint32_t(b);  // bitmap keys are below 2^31
-      int32_t* o = out + r * (g.ndim + 1);
-      for (int d = g.ndim - 1; d >= 0; --d) {
-        const uint32_t sd = uint32_t(g.out_shape[d]);
-        const uint32_t q = rem / sd;
-        o[d + 1] = int32_t(rem - q * sd);
-        rem = q;
+      int32_t co[5] = {0, 0, 0, 0, 0};  // (batch, x0, .., x3); the loop is unrolled, so the
+#pragma unroll                          // divisors stay in registers across rows
+      for (int d = 3; d >= 0; --d) {
+        if (d < g.ndim) {
+          const uint32_t q = div31(rem, g.out_div[d]);  // rem < 2^31
+          co[d + 1] = int32_t(rem - q * uint32_t(g.out_shape[d]));
+          rem = q;
+        }
       }
-      o[0] = int32_t(rem);
+      co[0] = int32_t(rem);
+      int32_t* o = out + r * (g.ndim + 1);
+      if (g.ndim == 3 && (reinterpret_cast<uintptr_t>(out) & 15u) == 0) {  // one 16-byte store
+        *reinterpret_cast<int4*>(o) = make_int4(co[0], co[1], co[2], co[3]);
+      } else {
+#pragma unroll
+        for (int d = 0; d < 5; ++d)
+          if (d <= g.ndim) o[d] = co[d];
+      }
       ++r;
     }
   }
@@ -1265,14 +1307,24 @@ __global__ void delinearize(const KeyT* __restrict__ keys, int64_t n, GeomDev g,
                             int32_t* __restrict__ out) {
   const int64_t r = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (r >= n) return;
-  uint64_t rem = uint64_t(keys[r]);
   int32_t* o = out + r * (g.ndim + 1);
-  for (int d = g.ndim - 1; d >= 0; --d) {
-    const uint64_t s = uint64_t(g.out_shape[d]);
-    o[d + 1] = int32_t(rem % s);
-    rem /= s;
+  if constexpr (sizeof(KeyT) == 4) {  // int32 keys: below 2^31, the multiply-shift division
+    uint32_t rem = uint32_t(keys[r]);
+    for (int d = g.ndim - 1; d >= 0; --d) {
+      const uint32_t q = div31(rem, g.out_div[d]);
+      o[d + 1] = int32_t(rem - q * uint32_t(g.out_shape[d]));
+      rem = q;
+    }
+    o[0] = int32_t(rem);
+  } else {
+    uint64_t rem = uint64_t(keys[r]);
+    for (int d = g.ndim - 1; d >= 0; --d) {
+      const uint64_t s = uint64_t(g.out_shape[d]);
+      o[d + 1] = int32_t(rem % s);
+      rem /= s;
+    }
+    o[0] = int32_t(rem);
   }
-  o[0] = int32_t(rem);
 }
 
 // One thread per input row j: pb[k, j] = output row of candidate (k, j) or -1,
