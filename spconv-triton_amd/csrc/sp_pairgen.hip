@@ -270,7 +270,9 @@ __global__ __launch_bounds__(256) void subm_insert_dense(const int32_t* __restri
   Coord c = load_coord(idx, r, g);
   if (!c.ok) return;
   int64_t acc = c.b;
-  for (int d = 0; d < g.ndim; ++d) acc = acc * g.in_shape[d] + c.x[d];
+#pragma unroll
+  for (int d = 0; d < 4; ++d)  // (unrolled: c.x stays in registers)
+    if (d < g.ndim) acc = acc * g.in_shape[d] + c.x[d];
   atomicMin(&grid[acc], int32_t(r));
 }
 
@@ -1310,10 +1312,13 @@ __global__ void delinearize(const KeyT* __restrict__ keys, int64_t n, GeomDev g,
   int32_t* o = out + r * (g.ndim + 1);
   if constexpr (sizeof(KeyT) == 4) {  // int32 keys: below 2^31, the multiply-shift division
     uint32_t rem = uint32_t(keys[r]);
-    for (int d = g.ndim - 1; d >= 0; --d) {
-      const uint32_t q = div31(rem, g.out_div[d]);
-      o[d + 1] = int32_t(rem - q * uint32_t(g.out_shape[d]));
-      rem = q;
+#pragma unroll
+    for (int d = 3; d >= 0; --d) {  // (unrolled: the divisors are loaded once)
+      if (d < g.ndim) {
+        const uint32_t q = div31(rem, g.out_div[d]);
+        o[d + 1] = int32_t(rem - q * uint32_t(g.out_shape[d]));
+        rem = q;
+      }
     }
     o[0] = int32_t(rem);
   } else {
