@@ -364,7 +364,8 @@ __device__ __forceinline__ void direct_tile(const T* __restrict__ A, const T* __
   const int E = G + kPad;
   const DirectLds L = direct_lds(E, uint32_t(sizeof(OutT)));
   uint32_t* s_kb = reinterpret_cast<uint32_t*>(smem + L.kb_off) + wave * E;
-  int32_t* s_src = reinterpret_cast<int32_t*>(smem + L.src_off) + wave * E * 64;
+  // byte offset in A of each (item, row) source row, kOob for none
+  uint32_t* s_src = reinterpret_cast<uint32_t*>(smem + L.src_off) + wave * E * 64;
 
   const uint32_t row_bytes = uint32_t(R) * ES;
   const uint32_t slab_bytes = uint32_t(N) * V * ES;        // one (offset, r / V) slab of Bt
@@ -400,7 +401,11 @@ __device__ __forceinline__ void direct_tile(const T* __restrict__ A, const T* __
         m_lo |= __shfl_xor(m_lo, off, 64);
         m_hi |= __shfl_xor(m_hi, off, 64);
       }
-      uint64_t live = (uint64_t(m_hi) << 32) | m_lo;  // wave-uniform
+      // wave-uniform after the reduction; readfirstlane puts it (and the batch
+      // loop below, and so nact) in scalar registers
+      m_lo = __builtin_amdgcn_readfirstlane(m_lo);
+      m_hi = __builtin_amdgcn_readfirstlane(m_hi);
+      uint64_t live = (uint64_t(m_hi) << 32) | m_lo;
       if (kn < 64) live &= (uint64_t(1) << kn) - 1u;
       while (live) {  // a batch of the lowest set offsets, ascending
         int us[kTabBatch];
@@ -421,7 +426,7 @@ __device__ __forceinline__ void direct_tile(const T* __restrict__ A, const T* __
         for (int b = 0; b < kTabBatch; ++b) {
           const bool ok = row_ok && us[b] >= 0 && v[b] >= 0 && v[b] < n_src;
           if (us[b] >= 0 && __ballot(ok)) {  // wave-uniform
-            s_src[(nact * 32 + l32) * 2 + h] = ok ? v[b] : -1;
+            s_src[(nact * 32 + l32) * 2 + h] = ok ? uint32_t(v[b]) * row_bytes : kOob;
             if (lane == 0) s_kb[nact] = uint32_t(kc + us[b]) * k_bytes;
             ++nact;
           }
@@ -441,7 +446,8 @@ __device__ __forceinline__ void direct_tile(const T* __restrict__ A, const T* __
         for (int u = 0; u < kTabBatch; ++u) {
           const bool ok = row_ok && u0 + u < kn && v[u] >= 0 && v[u] < n_src;
           if (u0 + u < kn && __ballot(ok)) {  // wave-uniform
-            s_src[(nact * 32 + l32) * 2 + h] = ok ? v[u] : -1;  // [item][l32][mt], mt = lane / 32
+            // [item][l32][mt], mt = lane / 32
+            s_src[(nact * 32 + l32) * 2 + h] = ok ? uint32_t(v[u]) * row_bytes : kOob;
             if (lane == 0) s_kb[nact] = uint32_t(kc + u0 + u) * k_bytes;
             ++nact;
           }
@@ -450,78 +456,101 @@ __device__ __forceinline__ void direct_tile(const T* __restrict__ A, const T* __
     }
 #pragma unroll
     for (int q = 0; q < kPad; ++q) {  // padding items: no source row, out-of-range B
-      s_src[((nact + q) * 32 + l32) * 2 + h] = -1;
+      s_src[((nact + q) * 32 + l32) * 2 + h] = kOob;
       if (lane == 0) s_kb[nact + q] = kBOob;
     }
 
-    for (int rc = 0; rc < nrc; ++rc) {
-      // Step `it`: the A loads of item it+1 and the table entries of item it+2,
-      // then the MFMAs of item it, then the B loads of item it+2.
-      uint32_t bl[2][2];  // this lane's B offsets inside an offset's slabs
+    nact = __builtin_amdgcn_readfirstlane(nact);  // wave-uniform: the cursors below are scalar
+    if (nact == 0) continue;                      // no pair in this wave's rows
+    // The group's (chunk, item) steps as one software pipeline, chunk by chunk
+    // and items ascending inside a chunk (the summation order of every
+    // kernel).  A cursor walks items 0 .. nact - 1 of chunks 0 .. nrc - 1 and
+    // then runs on into the padding items of the last chunk, whose loads read
+    // zeros, so no chunk restarts the pipeline.  Step j: the A loads of step
+    // j + 1, the MFMAs of step j, the B loads of step j + 2.
+    struct Cur {
+      int rc, it;
+    };
+    auto advance = [&](Cur& c) {
+      if (++c.it == nact && c.rc + 1 < nrc) {
+        c.it = 0;
+        ++c.rc;
+      }
+    };
+    uint32_t bl[2][2];  // this lane's B offsets inside chunk 0 of an offset's slabs
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) bl[ks][nt] = bcol[nt] + uint32_t(ks * 2 + h) * slab_bytes;
+    const uint32_t chunk_b = 4u * slab_bytes;  // B bytes per chunk of an offset
+    auto entry = [&](int it) -> uint2 {
+      return *reinterpret_cast<const uint2*>(s_src + (it * 32 + l32) * 2);
+    };
+    auto load_b = [&](uint32_t kb, int rc, frag (&b)[2][2]) {
+      const uint32_t kr = kb + uint32_t(rc) * chunk_b;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-          bl[ks][nt] = bcol[nt] + uint32_t(rc * 4 + ks * 2 + h) * slab_bytes;
-      auto entry = [&](int it) -> int2 {
-        return *reinterpret_cast<const int2*>(s_src + (it * 32 + l32) * 2);
-      };
-      auto load_b = [&](uint32_t kb, frag (&b)[2][2]) {
+        for (int nt = 0; nt < 2; ++nt) b[ks][nt] = buf_frag<T>(rb, kr + bl[ks][nt]);
+    };
+    auto load_a = [&](const uint2& e, int rc, frag (&a)[2][2]) {
+      const uint32_t s2[2] = {e.x, e.y};
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < 2; ++ks) {
+        const int e0 = rc * kChunk + (ks * 2 + h) * V;  // first element of this lane's piece
 #pragma unroll
-          for (int nt = 0; nt < 2; ++nt) b[ks][nt] = buf_frag<T>(rb, kb + bl[ks][nt]);
-      };
-      auto load_a = [&](const int2& e, frag (&a)[2][2]) {
-        const int32_t s2[2] = {e.x, e.y};
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const int e0 = rc * kChunk + (ks * 2 + h) * V;  // first element of this lane's piece
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt) {
-            const uint32_t base = s2[mt] >= 0 ? uint32_t(s2[mt]) * row_bytes : kOob;
-            if (VEC)
-              a[ks][mt] =
-                  buf_frag<T>(ra, (base != kOob && e0 < R) ? base + uint32_t(e0) * ES : kOob);
-            else
-              a[ks][mt] = buf_frag_elems<T>(ra, base, e0, R);
-          }
+        for (int mt = 0; mt < 2; ++mt) {
+          const uint32_t base = s2[mt];
+          if (VEC)
+            a[ks][mt] =
+                buf_frag<T>(ra, (base != kOob && e0 < R) ? base + uint32_t(e0) * ES : kOob);
+          else
+            a[ks][mt] = buf_frag_elems<T>(ra, base, e0, R);
         }
-      };
-      frag b0[2][2], b1[2][2], b2[2][2], a0[2][2], a1[2][2], a2[2][2];
-      int2 e_next;
-      {
-        const uint32_t k0 = s_kb[0], k1 = s_kb[1];
-        const int2 e0 = entry(0);
-        e_next = entry(1);
-        __builtin_amdgcn_sched_barrier(0);
-        load_b(k0, b0);
-        __builtin_amdgcn_sched_barrier(0);
-        load_b(k1, b1);
-        __builtin_amdgcn_sched_barrier(0);
-        load_a(e0, a0);
-        __builtin_amdgcn_sched_barrier(0);
       }
-      auto step = [&](int it, frag (&bc)[2][2], frag (&bn)[2][2], frag (&ac)[2][2],
-                      frag (&an)[2][2]) {
-        load_a(e_next, an);
-        const uint32_t k2 = s_kb[it + 2];
-        const int2 e2 = entry(it + 2);
-        __builtin_amdgcn_sched_barrier(0);
-        mma_item<T>(ac, bc, acc);
-        __builtin_amdgcn_sched_barrier(0);
-        load_b(k2, bn);
-        __builtin_amdgcn_sched_barrier(0);
-        e_next = e2;
-      };
-      step(0, b0, b2, a0, a1);
-      step(1, b1, b0, a1, a2);
-      step(2, b2, b1, a2, a0);
-      for (int it = 3; it < nact; it += 3) {  // reads entries up to max(nact + 3, 4) < nact + kPad
-        step(it, b0, b2, a0, a1);
-        step(it + 1, b1, b0, a1, a2);
-        step(it + 2, b2, b1, a2, a0);
-      }
+    };
+    frag b0[2][2], b1[2][2], b2[2][2], a0[2][2], a1[2][2], a2[2][2];
+    Cur ca{0, 0}, cb{0, 0};  // the steps of the next A and the next B loads
+    uint2 e_next;            // table entries of the next A loads' step
+    {
+      const uint32_t k0 = s_kb[0];
+      const int rc0 = cb.rc;
+      advance(cb);
+      const uint32_t k1 = s_kb[cb.it];
+      const int rc1 = cb.rc;
+      advance(cb);
+      const uint2 e0 = entry(0);
+      advance(ca);
+      __builtin_amdgcn_sched_barrier(0);
+      load_b(k0, rc0, b0);
+      __builtin_amdgcn_sched_barrier(0);
+      load_b(k1, rc1, b1);
+      __builtin_amdgcn_sched_barrier(0);
+      load_a(e0, 0, a0);
+      e_next = entry(ca.it);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    auto step = [&](frag (&bc)[2][2], frag (&bn)[2][2], frag (&ac)[2][2], frag (&an)[2][2]) {
+      load_a(e_next, ca.rc, an);
+      advance(ca);
+      const uint32_t kb = s_kb[cb.it];
+      const int rcb = cb.rc;
+      advance(cb);
+      const uint2 e2 = entry(ca.it);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_item<T>(ac, bc, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      load_b(kb, rcb, bn);
+      __builtin_amdgcn_sched_barrier(0);
+      e_next = e2;
+    };
+    // Steps 0 .. 3 ceil(S / 3) - 1 for S = nrc * nact: the cursors reach at most
+    // item nact + 3 of the last chunk, inside the kPad padding items.
+    const int n_steps = nrc * nact;
+    for (int j = 0; j < n_steps; j += 3) {
+      step(b0, b2, a0, a1);
+      step(b1, b0, a1, a2);
+      step(b2, b1, a2, a0);
     }
   }
   __syncthreads();  // the tables are free for the epilogue
