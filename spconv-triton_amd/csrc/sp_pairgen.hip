@@ -1118,6 +1118,9 @@ __device__ __forceinline__ void wave_count(uint32_t cnt, unsigned long long* tot
 // candidates of a row come in key order along the fastest dimension, so runs
 // in one word are ORed together before the atomic.
 // The candidates (the table's pairs) are counted into *npairs.
+// (Measured with each row's offsets split over four threads, as conv_fill_bitmap
+// does: 31.5 -> 54.3 us on the LiDAR encoder's first k3 s2 layer, the rows'
+// atomics meeting on the same bitmap words at the same time.)
 __global__ __launch_bounds__(256) void conv_mark(const int32_t* __restrict__ idx, int64_t n,
                                                  GeomDev g, uint32_t* __restrict__ bits,
                                                  unsigned long long* __restrict__ npairs) {
@@ -1146,6 +1149,32 @@ __global__ __launch_bounds__(256) void conv_mark(const int32_t* __restrict__ idx
   wave_count(cnt, npairs);
 }
 
+// conv_fill_bitmap splits each input row's kv offsets over the four waves of
+// a workgroup: wave w of workgroup b takes rows 64 b .. 64 b + 63 (one per
+// lane) and the contiguous offsets [w * per, (w + 1) * per), per =
+// ceil(kv / 4).  With one thread walking all kv offsets of its row the launch
+// held too few waves to hide the loop's latency (50k rows: 782 waves on 1 024
+// SIMDs): 26.4 -> 15.2 us on the LiDAR encoder's first k3 s2 layer.
+constexpr int kBitmapRowsPerBlock = 64;
+constexpr int kBitmapParts = 4;  // waves per workgroup, each a part of the offsets
+
+// First offset of this wave's part, its end, and its per-dimension offsets.
+__device__ __forceinline__ void offset_part(const GeomDev& g, int part, int* k0, int* k1,
+                                            int (&off)[4]) {
+  const int per = (g.kv + kBitmapParts - 1) / kBitmapParts;
+  *k0 = part * per < g.kv ? part * per : g.kv;
+  *k1 = *k0 + per < g.kv ? *k0 + per : g.kv;
+  int rem = *k0;
+#pragma unroll
+  for (int d = 3; d >= 0; --d) {  // the odometer order: the last dimension fastest
+    off[d] = 0;
+    if (d < g.ndim) {
+      off[d] = rem % g.ks[d];
+      rem /= g.ks[d];
+    }
+  }
+}
+
 // Output row of a marked key.
 __device__ __forceinline__ int64_t bitmap_rank(const uint32_t* __restrict__ bits,
                                                const uint32_t* __restrict__ prefix, uint64_t key) {
@@ -1154,33 +1183,52 @@ __device__ __forceinline__ int64_t bitmap_rank(const uint32_t* __restrict__ bits
   return int64_t(prefix[w]) + __popc(below);
 }
 
-// conv_fill with the bitmap's ranks.
+// conv_fill with the bitmap's ranks.  The rows' mask words (bit k of word
+// k / 32: offset k has a pair) are gathered from the four parts in the
+// dynamic LDS, mic * 64 words (launched with none when words is null).
 __global__ __launch_bounds__(256) void conv_fill_bitmap(
     const int32_t* __restrict__ idx, int64_t n, GeomDev g, const uint32_t* __restrict__ bits,
     const uint32_t* __restrict__ prefix, int64_t n_keep, int32_t* __restrict__ pf,
     int32_t* __restrict__ pb, uint32_t* __restrict__ words, int mic) {
-  const int64_t j = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (j >= n) return;
-  const Coord c = load_coord(idx, j, g);
-  int off[4] = {0, 0, 0, 0};
-  uint32_t word = 0;
-  for (int k = 0; k < g.kv; ++k) {
-    uint64_t key;
-    int32_t r = -1;
-    if (candidate_key<int32_t>(g, c, off, &key)) {
-      const int64_t rank = bitmap_rank(bits, prefix, key);
-      r = rank < n_keep ? int32_t(rank) : -1;
+  extern __shared__ uint32_t s_words[];  // [mic][64]
+  const int lane = int(threadIdx.x & 63);
+  const int64_t j = int64_t(blockIdx.x) * kBitmapRowsPerBlock + lane;
+  if (words) {
+    for (int i = int(threadIdx.x); i < mic * kBitmapRowsPerBlock; i += blockDim.x)
+      s_words[i] = 0u;
+    __syncthreads();
+  }
+  if (j < n) {
+    const Coord c = load_coord(idx, j, g);
+    int off[4], k0, k1;
+    offset_part(g, int(threadIdx.x >> 6), &k0, &k1, off);
+    uint32_t word = 0;
+    for (int k = k0; k < k1; ++k) {
+      uint64_t key;
+      int32_t r = -1;
+      if (candidate_key<int32_t>(g, c, off, &key)) {
+        const int64_t rank = bitmap_rank(bits, prefix, key);
+        r = rank < n_keep ? int32_t(rank) : -1;
+      }
+      if (r >= 0) {
+        if (pf) pf[int64_t(k) * n_keep + r] = int32_t(j);
+        word |= 1u << (k & 31);
+      }
+      if (pb) pb[int64_t(k) * n + j] = r;
+      if (((k & 31) == 31 || k == k1 - 1) && word) {
+        if (words) atomicOr(&s_words[(k >> 5) * kBitmapRowsPerBlock + lane], word);
+        word = 0;
+      }
+      odometer_next(g, off);
     }
-    if (r >= 0) {
-      if (pf) pf[int64_t(k) * n_keep + r] = int32_t(j);
-      word |= 1u << (k & 31);
+  }
+  if (words) {
+    __syncthreads();
+    for (int i = int(threadIdx.x); i < mic * kBitmapRowsPerBlock; i += blockDim.x) {
+      const int r = i / mic, w = i % mic;  // row-major: consecutive threads, consecutive words
+      const int64_t jr = int64_t(blockIdx.x) * kBitmapRowsPerBlock + r;
+      if (jr < n) words[jr * mic + w] = s_words[w * kBitmapRowsPerBlock + r];
     }
-    if (pb) pb[int64_t(k) * n + j] = r;
-    if ((k & 31) == 31 || k == g.kv - 1) {
-      if (words) words[j * mic + (k >> 5)] = word;
-      word = 0;
-    }
-    odometer_next(g, off);
   }
 }
 
@@ -1707,9 +1755,9 @@ int sp_pairgen_conv_fill(const sp_geom* g, const int32_t* indices, int64_t n, co
   if (conv_bitmap(d, n, key64)) {
     BitmapWs b;
     bitmap_layout(c, d, &b);
-    conv_fill_bitmap<<<unsigned(cdiv(n, 256)), 256, 0, s>>>(indices, n, d, b.bits, b.prefix,
-                                                            n_keep, pair_fwd, pair_bwd,
-                                                            mask_words_bwd, mic);
+    const size_t lds = mask_words_bwd ? size_t(mic) * kBitmapRowsPerBlock * 4 : 0;  // <= 32 KiB
+    conv_fill_bitmap<<<unsigned(cdiv(n, kBitmapRowsPerBlock)), 256, lds, s>>>(
+        indices, n, d, b.bits, b.prefix, n_keep, pair_fwd, pair_bwd, mask_words_bwd, mic);
     SP_LAUNCHED();
     emit_bitmap_keys<<<unsigned(cdiv(b.words, 1024)), 256, 0, s>>>(b.bits, b.prefix, b.words, d,
                                                                    n_keep, out_indices);

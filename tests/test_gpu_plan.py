@@ -452,8 +452,8 @@ def _orders(a, w, bias, transpose, pairs, M):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("case", ["subm", "strided", "kv125", "kv125_chunks", "sparse_wide",
-                                  "transposed", "subm_long"])
+@pytest.mark.parametrize("case", ["subm", "strided", "kv125", "kv125_chunks", "kv175", "kv245",
+                                  "sparse_wide", "transposed", "subm_long"])
 def test_mask_row_order_bit_identical(case, dtype):
     """Every row sums its offsets in ascending order whatever tile it falls in,
     so the mask-ordered GEMM (staged, overflow and direct tiles, and the thin
@@ -463,7 +463,9 @@ def test_mask_row_order_bit_identical(case, dtype):
     16-bit thin kernel gives its direct tiles to direct_tile, and a dgrad grid
     of 235, where it splits them into quarters.  kv125_chunks: 125 offsets
     (two of the direct kernel's groups of 64) over several reduction chunks,
-    where only tiles whose items lie in one group are planned."""
+    where only tiles whose items lie in one group are planned.  kv175 and
+    kv245 (5 x 5 x 7 and 5 x 7 x 7 windows): three and four groups, on a
+    sparse cloud (a few live offsets per wave) and a dense one."""
     from spconv_triton.pytorch._impl import gemm
 
     rng = np.random.default_rng(44)
@@ -477,6 +479,10 @@ def test_mask_row_order_bit_identical(case, dtype):
         grid, n, stride, ks = 20, 2500, 1, 5
     elif case == "kv125_chunks":
         grid, n, stride, ks, C, K = 40, 2000, 1, 5, 96, 64
+    elif case == "kv175":  # sparse
+        grid, n, stride, ks, C, K = 30, 500, 1, (5, 5, 7), 40, 48
+    elif case == "kv245":  # dense
+        grid, n, stride, ks, C, K = 24, 2000, 1, (5, 7, 7), 72, 48
     elif case == "subm_long":
         grid, n, stride, C, K = 48, 60000, 1, 32, 320
     elif case == "transposed":  # about one pair per output: thin tiles; 2 column blocks
@@ -487,12 +493,13 @@ def test_mask_row_order_bit_identical(case, dtype):
     subm = stride == 1
     from spconv_triton.core import ConvAlgo
     from spconv_triton.pytorch import ops
+    ksz = list(ks) if isinstance(ks, tuple) else [ks] * 3
     res = ops.get_indice_pairs_implicit_gemm(torch.from_numpy(idx).to(DEV), 2, [grid] * 3,
-                                             ConvAlgo.MaskImplicitGemm, [ks] * 3, [stride] * 3,
-                                             [0 if transpose else ks // 2] * 3, [1] * 3,
+                                             ConvAlgo.MaskImplicitGemm, ksz, [stride] * 3,
+                                             [0 if transpose else k // 2 for k in ksz], [1] * 3,
                                              [0] * 3, subm, transpose, is_train=True)
     pf, pb = res[2], res[3]
-    kv = ks ** 3
+    kv = int(np.prod(ksz))
     torch.manual_seed(3)
     x, _ = _q(torch.randn(idx.shape[0], C), dtype)
     w, _ = _q(torch.randn(K, kv, C) / np.sqrt(kv * C), dtype)
