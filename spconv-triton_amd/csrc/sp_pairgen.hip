@@ -1108,10 +1108,29 @@ static void bitmap_layout(W& w, const GeomDev& g, BitmapWs* out) {
   if (out) *out = BitmapWs{bits, prefix, total, sws, words};
 }
 
-// Adds every lane's count to *total with one atomic per wave.
-__device__ __forceinline__ void wave_count(uint32_t cnt, unsigned long long* total) {
+// Pair counts go to kCountSpread 64-bit counters, one atomic per workgroup on
+// counter blockIdx.x % kCountSpread; the reader sums them (count_sum).  Atomics
+// on one address serialise: one per wave onto a single counter took ~25 us of
+// conv_mark's 31 us on the LiDAR encoder's first k3 s2 layer (1 250 waves).
+// Every thread of the workgroup must call it (it has barriers).
+constexpr int kCountSpread = 16;
+__device__ __forceinline__ void block_count(uint32_t cnt, unsigned long long* counters) {
+  __shared__ uint32_t s_cnt;
   for (int off = 32; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
-  if (lane_id() == 0 && cnt != 0) atomicAdd(total, (unsigned long long)cnt);
+  if (threadIdx.x == 0) s_cnt = 0;
+  __syncthreads();
+  if (lane_id() == 0 && cnt != 0) atomicAdd(&s_cnt, cnt);
+  __syncthreads();
+  if (threadIdx.x == 0 && s_cnt != 0)
+    atomicAdd(&counters[blockIdx.x % kCountSpread], (unsigned long long)s_cnt);
+}
+
+// The total of the counters block_count adds to, from their host copy
+// (2 * kCountSpread 32-bit words, little-endian halves).
+static int64_t count_sum(const uint32_t* h) {
+  uint64_t t = 0;
+  for (int i = 0; i < kCountSpread; ++i) t += uint64_t(h[2 * i]) | (uint64_t(h[2 * i + 1]) << 32);
+  return int64_t(t);
 }
 
 // One thread per input row j: set the bits of its candidate outputs.  The kv
@@ -1146,7 +1165,7 @@ __global__ __launch_bounds__(256) void conv_mark(const int32_t* __restrict__ idx
     }
     if (cb != 0) atomicOr(&bits[cw], cb);
   }
-  wave_count(cnt, npairs);
+  block_count(cnt, npairs);
 }
 
 // conv_fill_bitmap splits each input row's kv offsets over the four waves of
@@ -1335,7 +1354,7 @@ __global__ __launch_bounds__(256) void conv_insert(const int32_t* __restrict__ i
     }
     odometer_next(g, off);
   }
-  wave_count(cnt, npairs);
+  block_count(cnt, npairs);
 }
 
 template <class Table, typename KeyT>
@@ -1649,19 +1668,19 @@ int sp_pairgen_conv_build(const sp_geom* g, const int32_t* indices, int64_t n, v
     fill_i32x4<<<unsigned(fb < 4096 ? fb : 4096), 256, 0, s>>>(
         reinterpret_cast<int32_t*>(b.bits), b.words, 0);
     SP_LAUNCHED();
-    // total[0]: set bits (from the scan); total[32..33]: the pair count
+    // total[0]: set bits (from the scan); total[32..63]: the pair counters
     auto* npairs = reinterpret_cast<unsigned long long*>(b.total + 32);
-    SP_HIP(hipMemsetAsync(npairs, 0, sizeof(unsigned long long), s));
+    SP_HIP(hipMemsetAsync(npairs, 0, kCountSpread * sizeof(unsigned long long), s));
     conv_mark<<<unsigned(cdiv(n, 256)), 256, 0, s>>>(indices, n, d, b.bits, npairs);
     SP_LAUNCHED();
     SP_CHECK_ARG(cdiv(b.words, 256) <= kMaxGridX, "pairgen: output volume too large");
     rc = exclusive_scan_popc(b.bits, b.prefix, b.words, b.total, b.scan_ws, s);
     if (rc) return rc;
-    uint32_t h[34] = {};
+    uint32_t h[32 + 2 * kCountSpread] = {};
     SP_HIP(hipMemcpyAsync(h, b.total, sizeof(h), hipMemcpyDeviceToHost, s));
     SP_HIP(hipStreamSynchronize(s));
     *n_out = int64_t(h[0]);
-    if (n_pairs) *n_pairs = int64_t(uint64_t(h[32]) | (uint64_t(h[33]) << 32));
+    if (n_pairs) *n_pairs = count_sum(h + 32);
     return SP_OK;
   }
   ConvWs w;
@@ -1684,13 +1703,13 @@ int sp_pairgen_conv_build(const sp_geom* g, const int32_t* indices, int64_t n, v
         indices, n, d, t, static_cast<uint32_t*>(w.list), w.counter, w.bound, npairs);
   }
   SP_LAUNCHED();
-  uint32_t host[34] = {};  // counter[0]: unique keys, [32..33]: pairs
+  uint32_t host[32 + 2 * kCountSpread] = {};  // counter[0]: unique keys, [32..63]: pairs
   uint32_t overflow = 0;
   SP_HIP(hipMemcpyAsync(host, w.counter, sizeof(host), hipMemcpyDeviceToHost, s));
   SP_HIP(hipMemcpyAsync(&overflow, w.flags, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
   SP_HIP(hipStreamSynchronize(s));
   if (overflow) return set_error(SP_ERR_HASH_FULL, "pairgen: coordinate hash overflow");
-  if (n_pairs) *n_pairs = int64_t(uint64_t(host[32]) | (uint64_t(host[33]) << 32));
+  if (n_pairs) *n_pairs = count_sum(host + 32);
   const int64_t cnt = int64_t(host[0]);
   if (cnt > w.bound) return set_error(SP_ERR_HASH_FULL, "pairgen: %lld keys > bound %lld",
                                       (long long)cnt, (long long)w.bound);
