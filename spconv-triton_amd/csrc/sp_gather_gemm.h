@@ -726,17 +726,26 @@ __host__ __device__ inline StagedLds staged_lds(int E, uint32_t out_size) {
   return l;
 }
 
+// SPLIT instances (one column block, N <= 64) take the last n_split tiles,
+// which would otherwise run as a round of their own on n_split CUs after the
+// others have finished, in quarters by the direct path (direct_quarter,
+// bit-identical): the grid's first staged_split_extra(n_split) workgroups take
+// the quarters (starting first, they finish early), the rest the other tiles.
+__host__ __device__ inline int64_t staged_split_extra(int n_split) {
+  return 8 * ((4 * int64_t(n_split) + 7) / 8);  // a multiple of 8 keeps the XCD mapping
+}
+
 // Every tile of a planned call (kv <= kPlanMaxKv): staged when its distinct
 // rows fit in LDS and its items (at most kPlanMaxItems, in one group of
 // kGroupOffsets offsets) are listed, else (an overflow tile) by the direct
 // path.  ORDERED as
 // for the direct kernel.
-template <typename T, typename OutT, bool VEC, bool ORDERED>
+template <typename T, typename OutT, bool VEC, bool ORDERED, bool SPLIT = false>
 __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
     const T* __restrict__ A, const T* __restrict__ Bt, const int32_t* __restrict__ pairs,
     const int32_t* __restrict__ order_arg, PlanDev plan, const float* __restrict__ bias,
     OutT* __restrict__ out, GemmBufs nb, int64_t n_src, int64_t M, int N, int R, int Rp,
-    int kv) {
+    int kv, int n_split) {
   const int32_t* __restrict__ order = ORDERED ? order_arg : nullptr;
   using frag = typename Mfma<T>::frag;
   constexpr int V = Mfma<T>::V;
@@ -753,7 +762,21 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
   const int h = lane >> 5, l32 = lane & 31;
   int64_t tile;
   int n0;
-  if (!staged_tile(M, N, &tile, &n0)) return;
+  if constexpr (SPLIT) {  // one column block
+    const int64_t n_extra = staged_split_extra(n_split);
+    const int64_t nt_main = (M + kTileRows - 1) / kTileRows - n_split;
+    if (blockIdx.x < n_extra) {  // whole workgroup (uniform)
+      const int64_t e = blockIdx.x;
+      if (e >= 4 * int64_t(n_split)) return;
+      direct_quarter<T, OutT, VEC>(A, Bt, pairs, bias, out, nb, n_src, M, N, R, Rp, kv,
+                                   nt_main + e / 4, int(e % 4), 0, smem, order);
+      return;
+    }
+    tile = xcd_tile(int64_t(blockIdx.x) - n_extra, nt_main);
+    n0 = 0;
+  } else {
+    if (!staged_tile(M, N, &tile, &n0)) return;
+  }
   const int64_t slot0 = tile * kTileRows + wave * 64;
 
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(A, nb.a_bytes);

@@ -560,19 +560,56 @@ static uint32_t staged_kernel_lds(int E, int kv, uint32_t out_size) {
   return a > b ? a : b;
 }
 
+// Compute units of the current device (cached per process: the one-GPU boxes
+// this targets hold one kind of device).
+static int device_cus() {
+  static int n = 0;
+  if (n <= 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+      n = v;
+    else
+      n = 256;
+  }
+  return n;
+}
+
+// A staged grid of one column block whose tile count exceeds a multiple of the
+// CU count by at most kStagedSplitMax tiles splits those last tiles into
+// quarters (gather_gemm_staged's SPLIT instances): run whole, they make a
+// last round on as many CUs that the rest of the chip waits for.  Measured on
+// the 64 -> 64 surface-cloud layer (256 CUs, tiles past 2 or 3 rounds of 256):
+// 14 past 768 (the 200k-voxel metric) 49.6 -> 47.9 us, 32 past 768 50.4 ->
+// 48.2, 40 past 512 38.8 -> 37.5, 64 past 512 38.9 -> 38.6, 96 past 512
+// 39.3 -> 44.8 (the quarters' direct gathers then cost more than the round).
+constexpr int kStagedSplitMax = 48;
+
 template <typename T, typename OutT, bool VEC>
 static int launch_staged(dim3 grid, hipStream_t s, const T* A, const T* bt, const int32_t* pairs,
                          OutT* o, GemmBufs nb, const GemmCall& c) {
   const uint32_t lds = staged_kernel_lds(c.plan.E, c.kv, uint32_t(sizeof(OutT)));
-  auto kern = c.order ? gather_gemm_staged<T, OutT, VEC, true>
-                      : gather_gemm_staged<T, OutT, VEC, false>;
-  static bool attr_set[2] = {false, false};  // per kernel instance
+  int n_split = 0;
+  if (!c.order && c.N <= 64) {
+    const int64_t nt = cdiv(c.M, kTileRows), ncu = device_cus();
+    const int64_t rem = nt % ncu;
+    if (nt > ncu && rem > 0 && rem <= kStagedSplitMax) n_split = int(rem);
+  }
+  auto kern = n_split ? gather_gemm_staged<T, OutT, VEC, false, true>
+                      : (c.order ? gather_gemm_staged<T, OutT, VEC, true>
+                                 : gather_gemm_staged<T, OutT, VEC, false>);
+  static bool attr_set[3] = {false, false, false};  // per kernel instance
   int rc = allow_lds(reinterpret_cast<const void*>(kern),
                      staged_kernel_lds(plan_layout(1, kPlanMaxKv).E, kPlanMaxKv, uint32_t(sizeof(OutT))),
-                     attr_set[c.order ? 1 : 0]);
+                     attr_set[n_split ? 2 : (c.order ? 1 : 0)]);
   if (rc) return rc;
+  if (n_split) {  // the split tiles' quarters in front, the other tiles after them
+    const int64_t n_extra = staged_split_extra(n_split);
+    SP_CHECK_ARG(n_extra + grid.x - n_split <= kMaxGridX, "gemm: too many tiles");
+    grid.x = unsigned(n_extra + grid.x - n_split);
+  }
   kern<<<grid, 256, lds, s>>>(A, bt, pairs, c.order, c.plan, c.bias, o, nb, c.n_src, c.M, c.N,
-                              c.R, c.Rp, c.kv);
+                              c.R, c.Rp, c.kv, n_split);
   SP_LAUNCHED();
   return SP_OK;
 }

@@ -399,6 +399,29 @@ def test_planned_metric_shape():
     assert torch.equal(planned, direct)
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("extra", [1, 14, 48, 49])
+def test_planned_tail_tiles_split(extra, dtype):
+    """A one-column-block planned GEMM whose tile count exceeds the device's CU
+    count by 1..48 tiles runs those last tiles in quarters by the direct path
+    (the staged kernel's SPLIT instances; 49 does not split).  The result is
+    bit-identical to the unplanned GEMM, the last tile partial included."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    M = (cus + extra) * 256 - 17
+    rng = np.random.default_rng(500 + extra)
+    grid = 64
+    idx = rand_indices(rng, 1, [grid] * 3, M)
+    res = _tables(idx, 1, [grid] * 3, [3] * 3, [1] * 3, [1] * 3, True)
+    pf = res[2]
+    assert pf.shape[1] == M
+    torch.manual_seed(extra)
+    x, _ = _q(torch.randn(M, 48), dtype)
+    w, _ = _q(torch.randn(64, 27, 48) / np.sqrt(27 * 48), dtype)
+    b, _ = _q(torch.randn(64) * 0.1, dtype)
+    planned, direct = _both(x, w, b, False, pf, M)
+    assert torch.equal(planned, direct)
+
+
 # ---------------------------------------------------------------------------
 # row order: the GEMM over the rows in mask-argsort order
 # ---------------------------------------------------------------------------
