@@ -412,7 +412,7 @@ def main() -> int:
             "traffic": traffic,
             "traffic_source": "stored rocprofv3 FETCH_SIZE/WRITE_SIZE profile "
                               "(profiles/gather_gemm_traffic.json), not this run",
-            "kernel": "gather_gemm_staged<f16,f16,VEC>",
+            "kernel": "gather_gemm_staged<f16,f16,VEC,natural,SPLIT>",
             "kernel_ms": round(kernel_ms, 5),
             "kernel_ms_source": f"HIP events around {GEMM_LAUNCHES}-launch graphs of the GEMM "
                                 "alone, per launch",
