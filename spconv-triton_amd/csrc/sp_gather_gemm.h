@@ -634,37 +634,98 @@ __device__ __forceinline__ void direct_quarter(const T* __restrict__ A, const T*
       if (h == 0) s_src[(nact + pi) * 32 + l32] = -1;
       if (lane == 0) s_kb[nact + pi] = kBOob;
     }
-    for (int rc = 0; rc < nrc; ++rc) {
-      auto load = [&](int it, frag (&a)[2], frag (&b)[2]) {
-        const int32_t src = s_src[it * 32 + l32];
-        const uint32_t kb = s_kb[it];
-        const uint32_t base = src >= 0 ? uint32_t(src) * row_bytes : kOob;
+    if constexpr (sizeof(T) != 4) {
+      // 16-bit operands: one pipeline per 64-byte chunk (32 channels).  With
+      // 4-byte operands a chunk holds 16 channels, a row twice the chunks,
+      // and one pipeline over the group's (chunk, item) steps, as in
+      // direct_tile, measured faster: the reference-class fp32 layers' GEMM
+      // (thin kernel, quarters) subm 0.106 -> 0.102 ms, strided 0.601 ->
+      // 0.563, transposed 2.58 -> 2.50; the same for 16-bit operands made the
+      // metric's split tail quarters 0.6 us slower.
+      for (int rc = 0; rc < nrc; ++rc) {
+        auto load = [&](int it, frag (&a)[2], frag (&b)[2]) {
+          const int32_t src = s_src[it * 32 + l32];
+          const uint32_t kb = s_kb[it];
+          const uint32_t base = src >= 0 ? uint32_t(src) * row_bytes : kOob;
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const int e0 = rc * kChunk + (ks * 2 + h) * V;
-          if (VEC)
-            a[ks] = buf_frag<T>(ra, (base != kOob && e0 < R) ? base + uint32_t(e0) * ES : kOob);
-          else
-            a[ks] = buf_frag_elems<T>(ra, base, e0, R);
-          b[ks] = buf_frag<T>(rb, kb + bcol + uint32_t(rc * 4 + ks * 2 + h) * slab_bytes);
+          for (int ks = 0; ks < 2; ++ks) {
+            const int e0 = rc * kChunk + (ks * 2 + h) * V;
+            if (VEC)
+              a[ks] = buf_frag<T>(ra, (base != kOob && e0 < R) ? base + uint32_t(e0) * ES : kOob);
+            else
+              a[ks] = buf_frag_elems<T>(ra, base, e0, R);
+            b[ks] = buf_frag<T>(rb, kb + bcol + uint32_t(rc * 4 + ks * 2 + h) * slab_bytes);
+          }
+        };
+        // two items in flight: item it + 2 loads while item it multiplies
+        frag a0[2], b0[2], a1[2], b1[2], a2[2], b2[2];
+        load(0, a0, b0);
+        load(1, a1, b1);
+        auto step = [&](int it, frag (&ac)[2], frag (&bc)[2], frag (&an)[2], frag (&bn)[2]) {
+          load(it + 2, an, bn);
+          __builtin_amdgcn_sched_barrier(0);
+          Mfma<T>::mma(ac[0], bc[0], acc);
+          Mfma<T>::mma(ac[1], bc[1], acc);
+          __builtin_amdgcn_sched_barrier(0);
+        };
+        for (int it = 0; it < nact; it += 3) {  // reads entries up to nact + 4 < nact + kPad
+          step(it, a0, b0, a2, b2);
+          step(it + 1, a1, b1, a0, b0);
+          step(it + 2, a2, b2, a1, b1);
         }
-      };
-      // two items in flight: item it + 2 loads while item it multiplies
-      frag a0[2], b0[2], a1[2], b1[2], a2[2], b2[2];
-      load(0, a0, b0);
-      load(1, a1, b1);
-      auto step = [&](int it, frag (&ac)[2], frag (&bc)[2], frag (&an)[2], frag (&bn)[2]) {
-        load(it + 2, an, bn);
-        __builtin_amdgcn_sched_barrier(0);
-        Mfma<T>::mma(ac[0], bc[0], acc);
-        Mfma<T>::mma(ac[1], bc[1], acc);
-        __builtin_amdgcn_sched_barrier(0);
-      };
-      for (int it = 0; it < nact; it += 3) {  // reads entries up to nact + 4 < nact + kPad
-        step(it, a0, b0, a2, b2);
-        step(it + 1, a1, b1, a0, b0);
-        step(it + 2, a2, b2, a1, b1);
       }
+      continue;
+    }
+    nact = __builtin_amdgcn_readfirstlane(nact);  // wave-uniform: the cursor is scalar
+    if (nact == 0) continue;                      // no pair in this wave's rows
+    // The group's (chunk, item) steps as one pipeline, as in direct_tile: a
+    // cursor walks items 0 .. nact - 1 of chunks 0 .. nrc - 1, then the
+    // padding items after the last chunk.  Step j: the loads of step j + 2,
+    // the MFMAs of step j.
+    struct Cur {
+      int rc, it;
+    };
+    auto advance = [&](Cur& c) {
+      if (++c.it == nact && c.rc + 1 < nrc) {
+        c.it = 0;
+        ++c.rc;
+      }
+    };
+    auto load = [&](const Cur& c, frag (&a)[2], frag (&b)[2]) {
+      const int32_t src = s_src[c.it * 32 + l32];
+      const uint32_t kb = s_kb[c.it];
+      const uint32_t base = src >= 0 ? uint32_t(src) * row_bytes : kOob;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int e0 = c.rc * kChunk + (ks * 2 + h) * V;
+        if (VEC)
+          a[ks] = buf_frag<T>(ra, (base != kOob && e0 < R) ? base + uint32_t(e0) * ES : kOob);
+        else
+          a[ks] = buf_frag_elems<T>(ra, base, e0, R);
+        b[ks] = buf_frag<T>(rb, kb + bcol + uint32_t(c.rc * 4 + ks * 2 + h) * slab_bytes);
+      }
+    };
+    frag a0[2], b0[2], a1[2], b1[2], a2[2], b2[2];
+    Cur cl{0, 0};  // the step of the next loads
+    load(cl, a0, b0);
+    advance(cl);
+    load(cl, a1, b1);
+    advance(cl);
+    auto step = [&](frag (&ac)[2], frag (&bc)[2], frag (&an)[2], frag (&bn)[2]) {
+      load(cl, an, bn);
+      advance(cl);
+      __builtin_amdgcn_sched_barrier(0);
+      Mfma<T>::mma(ac[0], bc[0], acc);
+      Mfma<T>::mma(ac[1], bc[1], acc);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    // steps 0 .. 3 ceil(S / 3) - 1 for S = nrc * nact: the loads reach at most
+    // item nact + 3 after the last chunk, inside the kPad padding items
+    const int n_steps = nrc * nact;
+    for (int j = 0; j < n_steps; j += 3) {
+      step(a0, b0, a2, b2);
+      step(a1, b1, a0, b0);
+      step(a2, b2, a1, b1);
     }
   }
   // ---- epilogue: element stores (+ bias); rows past M and columns past N dropped
