@@ -837,6 +837,11 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
     n0 = 0;
   } else {
     if (!staged_tile(M, N, &tile, &n0)) return;
+    // with a row order, tiles in reverse, as in the thin kernel: in mask
+    // order the rows with the most mask bits come last, and their tiles (most
+    // items, and the overflow tiles the direct path takes) should start first
+    // rather than set the end
+    if constexpr (ORDERED) tile = (M + kTileRows - 1) / kTileRows - 1 - tile;
   }
   const int64_t slot0 = tile * kTileRows + wave * 64;
 

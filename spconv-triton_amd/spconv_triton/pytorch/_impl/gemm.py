@@ -181,19 +181,27 @@ def gather_plan(pairs: torch.Tensor, n_src: int, words: torch.Tensor | None = No
 #: reference's order (gemm.py:282-296), whose tiles hold rows with similar
 #: masks and so have fewer live offsets, but more distinct source rows (tiles
 #: whose rows do not fit in LDS are gathered directly).  "auto": natural,
-#: unless the layer is wide (C * K >= ORDER_MIN_WORK), the natural tiles spend
-#: less than ORDER_MAX_EFFICIENCY of their MFMA work on pairs, and the mask
-#: order cuts that work to at most ORDER_MAX_WORK_RATIO of it; only tables
-#: that wide layers use more than once are looked at (see row_order_variant).
-#: The efficiency test only saves the mask sort where the work test must fail
-#: (the mask order's work is at least the pairs), so the two bounds are equal:
-#: 50k uniform voxels in 41 x 1600 x 1408 (24 % of the natural work on pairs,
-#: mask order 28 % of the natural work) take the mask order.
-#: Every order gives bit-identical results.
+#: unless the layer is wide (C * K >= ORDER_MIN_WORK) and the mask order cuts
+#: the natural tiles' MFMA work to at most ORDER_MAX_WORK_RATIO of it; only
+#: tables that wide layers use more than once are looked at (see
+#: row_order_variant).  Before the mask sort, a table whose natural work is
+#: under 1 / ORDER_MAX_WORK_RATIO times its pairs is left natural (the mask
+#: order's work is at least the pairs): 50k uniform voxels in 41 x 1600 x
+#: 1408 (24 % of the natural work on pairs, mask order 28 % of the natural
+#: work) take the mask order.  Every order gives bit-identical results.
 ROW_ORDER = os.environ.get("SPCONV_GEMM_ROW_ORDER", "auto")
 ORDER_MIN_WORK = 128 * 128
-ORDER_MAX_EFFICIENCY = 0.35
 ORDER_MAX_WORK_RATIO = 0.35
+#: IEEE fp32 operands (no SPCONV_ALLOW_TF32): a 32x32x2 fp32 MFMA does 1/8
+#: of a 32x32x16 fp16 one's work in twice the clocks, so the matrix cores are
+#: the limit, and the kernels skip the MFMAs of 32-row blocks without a pair.
+#: The work is then also counted per live (64-row block, offset) pair, and the
+#: mask order is taken when it cuts that work to at most
+#: ORDER_MAX_WORK_RATIO_FP32 (or the tile count passes the rule above):
+#: the LiDAR-like 50k cloud (natural 64-row work 4.6x the pairs, mask order
+#: 49 % of it) 256 -> 256 GEMM 1.08 -> 0.71 ms, 128 -> 128 0.37 -> 0.23 ms,
+#: where the 256-row tile count (mask order 50 %) keeps 16-bit layers natural.
+ORDER_MAX_WORK_RATIO_FP32 = 0.6
 #: A strided or transposed convolution's rulebook is often used once (rebuilt
 #: every pass), so waiting for a second use would never reorder it.  Its pair
 #: generation counts the table's pairs in passing; a table with at most
@@ -285,10 +293,14 @@ def _decide_at_first_use(pairs: torch.Tensor, work: int) -> bool:
             and float(M) * kv * work >= FIRST_USE_MIN_MACS)
 
 
-def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool = True):
+def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool = True,
+                      fp32: bool = False):
     """(order, permuted table, its gather plan or None) when a GEMM of
     ``work`` = C * K on this table should take its rows in mask order (see
     ROW_ORDER), else None.  ``plan_ok``: the call may use a gather plan.
+    ``fp32``: the call multiplies IEEE fp32 operands (see
+    ORDER_MAX_WORK_RATIO_FP32); the call that makes the decision sets it for
+    every layer on the table.
 
     In auto mode only tables that wide layers use more than once are looked
     at (or, see FIRST_USE_MAX_PAIRS_PER_ROW, tables with few pairs per row):
@@ -335,20 +347,26 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool 
 
     planned = plan_ok and kv <= _ORDERED_PLAN_MAX_KV
 
-    def mfma_rows(stats):  # rows the GEMM multiplies: per live tile or wave offset
-        return 256 * stats[1] if planned else 64 * stats[2]
+    # (rows the GEMM multiplies, bound): per live tile offset (planned) or wave
+    # offset; fp32 operands also per live 64-row block offset.  The mask order
+    # is taken when one measure passes.  The efficiency test (pairs against
+    # the natural work) skips the mask sort only where its work test must
+    # fail, as the mask order's work is at least the pairs.
+    tests = [((lambda st: 256 * st[1]) if planned else (lambda st: 64 * st[2]),
+              ORDER_MAX_WORK_RATIO)]
+    if fp32:
+        tests.append((lambda st: 64 * st[2], ORDER_MAX_WORK_RATIO_FP32))
 
     variant = None
     npairs = getattr(pairs, "_spconv_triton_npairs", None)
     sure = mode == "mask" or (npairs is not None and npairs <= SURE_PAIRS_PER_ROW * M)
     natural = table_stats(pairs, n_src) if not sure else None
-    done = mfma_rows(natural) if natural is not None else 0
-    if sure or (done > 0 and natural[0] < ORDER_MAX_EFFICIENCY * done):
+    if sure or any(0 < natural[0] < r * f(natural) for f, r in tests):
         order, words = mask_order(pairs, with_words=True)
         perm = permute_table(pairs, order, words if kv <= 32 else None)
         perm._spconv_triton_words = words  # the unplanned kernel reads live offsets only
         masked = table_stats(perm, n_src) if not sure else None
-        if sure or mfma_rows(masked) <= ORDER_MAX_WORK_RATIO * done:
+        if sure or any(f(masked) <= r * f(natural) for f, r in tests):
             plan = gather_plan(perm, n_src, words) if planned else None
             tiles = (M + 255) // 256
             if (plan is not None and kv > _PLAN_MAX_KV
@@ -451,7 +469,8 @@ def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: 
     packed = packed_weight(filters, bias, "bf16x3" if split else a.dtype, transpose)
     L = _lib.lib()
     use_plan = _use_plan(M, C, K)
-    variant = row_order_variant(pairs, a.shape[0], K * C, use_plan)
+    variant = row_order_variant(pairs, a.shape[0], K * C, use_plan,
+                                fp32=a.dtype == torch.float32 and not split)
     if split:  # the GEMM's reduction dimension is tripled
         K, C = (3 * K, C) if transpose else (K, 3 * C)
     if variant is None:

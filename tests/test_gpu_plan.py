@@ -582,6 +582,56 @@ def test_auto_row_order_decision():
             assert pf._spconv_triton_order[1] == "natural"
 
 
+def test_row_order_decision_for_fp32_operands():
+    """IEEE fp32 operands count the work per live (64-row block, offset) pair:
+    on the LiDAR-like cloud (3.27 pairs per row) the mask order cuts that to
+    about half, so an fp32 layer takes it while a 16-bit one (256-row tile
+    count: 50 %) stays natural.  The mask-ordered fp32 forward equals the
+    natural one bit for bit and the fp64 oracle on sampled rows."""
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+    from spconv_triton.pytorch._impl import gemm
+
+    from bench_data import lidar_cloud
+
+    shape = [41, 1600, 1408]
+    idx = lidar_cloud(50000, batch=1, seed=0, shape=shape)
+    t = torch.from_numpy(idx).to(DEV)
+
+    def table():
+        return ops.get_indice_pairs_implicit_gemm(t, 1, shape, ConvAlgo.MaskImplicitGemm, [3] * 3,
+                                                  [1] * 3, [1] * 3, [1] * 3, [0] * 3, True, False,
+                                                  is_train=False)[2]
+
+    n = idx.shape[0]
+    C = K = 128
+    p16 = table()
+    for _ in range(2):
+        assert gemm.row_order_variant(p16, n, C * K, fp32=False) is None
+    assert p16._spconv_triton_order[1] == "natural"
+    pf = table()
+    assert gemm.row_order_variant(pf, n, C * K, fp32=True) is None  # the first call: "seen"
+    variant = gemm.row_order_variant(pf, n, C * K, fp32=True)
+    assert isinstance(variant, tuple), "the fp32 layer did not take the mask order"
+    order = variant[0]
+    assert torch.equal(torch.sort(order.long())[0], torch.arange(n, device=DEV))
+    torch.manual_seed(5)
+    x = torch.randn(n, C, device=DEV)
+    w = torch.randn(K, 27, C, device=DEV) / np.sqrt(27 * C)
+    out = gemm.conv_forward(x, w, pf, n)
+    prev = gemm.ROW_ORDER
+    gemm.ROW_ORDER = "natural"
+    try:
+        ref = gemm.conv_forward(x, w, table(), n)
+    finally:
+        gemm.ROW_ORDER = prev
+    assert torch.equal(out, ref)
+    rows = np.sort(np.random.default_rng(5).choice(n, 600, replace=False))
+    want = orc.gemm_fwd(x.cpu().numpy(), w.cpu().numpy(), pf.cpu().numpy()[:, rows])
+    got = out[torch.from_numpy(rows).to(DEV)].double().cpu().numpy()
+    assert np.abs(got - want).max() <= 1e-5 * max(1.0, float(np.abs(want).max()))  # fp32 rtol
+
+
 def test_row_order_decided_at_first_use_for_one_pair_per_row():
     """A transposed convolution of sparse voxels has about one pair per output
     row, and its rulebook is usually used once: the row order is decided at
