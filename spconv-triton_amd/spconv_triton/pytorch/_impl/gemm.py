@@ -202,6 +202,19 @@ ORDER_MAX_WORK_RATIO = 0.35
 #: 49 % of it) 256 -> 256 GEMM 1.08 -> 0.71 ms, 128 -> 128 0.37 -> 0.23 ms,
 #: where the 256-row tile count (mask order 50 %) keeps 16-bit layers natural.
 ORDER_MAX_WORK_RATIO_FP32 = 0.6
+#: Tables of at least ORDER_SPARSE_MIN_KV offsets with at most
+#: ORDER_SPARSE_MAX_PAIRS_PER_ROW pairs per row take the mask order up to
+#: ORDER_SPARSE_MAX_WORK_RATIO of the natural tile work: their mask-ordered
+#: tiles reference few enough distinct rows that about half of them still
+#: stage in LDS (the LiDAR-like 50k cloud, 3.27 pairs per row: 95 of 196
+#: tiles overflow), where a surface cloud's (10 pairs per row) nearly all
+#: overflow.  That cloud's SubMConv3d 256 -> 256 (tile work 50 %): fp16 0.149
+#: -> 0.117 ms, TF32-equivalent 0.406 -> 0.342 ms.  The k2 s2 tables of the
+#: ResUNet step (kv = 8, 1.7 pairs per row, 42 %; rebuilt every step) paid a
+#: mask sort per step for nothing (step +0.1 ms): smaller windows stay out.
+ORDER_SPARSE_MIN_KV = 27
+ORDER_SPARSE_MAX_PAIRS_PER_ROW = 4.0
+ORDER_SPARSE_MAX_WORK_RATIO = 0.5
 #: A strided or transposed convolution's rulebook is often used once (rebuilt
 #: every pass), so waiting for a second use would never reorder it.  Its pair
 #: generation counts the table's pairs in passing; a table with at most
@@ -361,6 +374,9 @@ def row_order_variant(pairs: torch.Tensor, n_src: int, work: int, plan_ok: bool 
     npairs = getattr(pairs, "_spconv_triton_npairs", None)
     sure = mode == "mask" or (npairs is not None and npairs <= SURE_PAIRS_PER_ROW * M)
     natural = table_stats(pairs, n_src) if not sure else None
+    if (natural is not None and kv >= ORDER_SPARSE_MIN_KV
+            and natural[0] <= ORDER_SPARSE_MAX_PAIRS_PER_ROW * M):
+        tests.append((tests[0][0], ORDER_SPARSE_MAX_WORK_RATIO))
     if sure or any(0 < natural[0] < r * f(natural) for f, r in tests):
         order, words = mask_order(pairs, with_words=True)
         perm = permute_table(pairs, order, words if kv <= 32 else None)

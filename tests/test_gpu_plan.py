@@ -582,12 +582,13 @@ def test_auto_row_order_decision():
             assert pf._spconv_triton_order[1] == "natural"
 
 
-def test_row_order_decision_for_fp32_operands():
+def test_row_order_decision_for_fp32_operands(monkeypatch):
     """IEEE fp32 operands count the work per live (64-row block, offset) pair:
     on the LiDAR-like cloud (3.27 pairs per row) the mask order cuts that to
-    about half, so an fp32 layer takes it while a 16-bit one (256-row tile
-    count: 50 %) stays natural.  The mask-ordered fp32 forward equals the
-    natural one bit for bit and the fp64 oracle on sampled rows."""
+    about half, so an fp32 layer takes it, while a 16-bit one (256-row tile
+    count: 50 %) takes it only through the band for sparse tables of 27 or
+    more offsets.  The mask-ordered fp32 forward equals the natural one bit
+    for bit and the fp64 oracle on sampled rows."""
     from spconv_triton.core import ConvAlgo
     from spconv_triton.pytorch import ops
     from spconv_triton.pytorch._impl import gemm
@@ -605,6 +606,10 @@ def test_row_order_decision_for_fp32_operands():
 
     n = idx.shape[0]
     C = K = 128
+    p16 = table()
+    assert gemm.row_order_variant(p16, n, C * K, fp32=False) is None
+    assert isinstance(gemm.row_order_variant(p16, n, C * K, fp32=False), tuple)
+    monkeypatch.setattr(gemm, "ORDER_SPARSE_MIN_KV", 28)  # the band off for kv = 27
     p16 = table()
     for _ in range(2):
         assert gemm.row_order_variant(p16, n, C * K, fp32=False) is None
