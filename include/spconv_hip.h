@@ -263,10 +263,14 @@ int sp_conv_gemm_planned(const void* a, int32_t dtype, int64_t n_src, const void
  * traversal, which visits rows in mask_argsort order so that a row tile holds
  * rows with similar masks (gemm.py:282-296, the mask_argsort operand of
  * _gather_gemm_kernel :501-568); with the table permuted up front the kernel
- * reads it coalesced.  thin_tiles != 0 (with a plan): most tiles of
+ * reads it coalesced.  thin_tiles 1 (with a plan): most tiles of
  * pairs_perm hold at most 4 live offsets (tables of about one pair per row);
  * a kernel that loads each chunk's rows and weights three chunks ahead runs
- * them (the others take the direct path inside it).  Results are the same.
+ * them (the others take the direct path inside it).  thin_tiles 2: the same
+ * kernel with every tile it hands to the direct path spread over four
+ * workgroups of a quarter of its rows each (fp32 operands on tables whose
+ * tiles mostly hold more offsets).  0: the staged kernel.  Results are the
+ * same; other values are an error.
  * row_words (nullable): the mask words of pairs_perm's rows, words_per_row
  * (>= ceil(kv / 32)) per row (bit k of row i set iff pairs_perm[k, i] >= 0,
  * e.g. the sorted pair_mask of sp_mask_sort whose argsort is row_order); an

@@ -1205,7 +1205,7 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_thin(
     int q_lo = 0, q_hi = 0;  // quarters [q_lo, q_hi) by the direct path
     if (blockIdx.x < n_extra) {
       const int64_t e = blockIdx.x;
-      if (e >= 3 * n_split * gy) return;
+      if (e >= 3 * int64_t(n_split) * gy) return;
       const int64_t tc = e / 3;  // (tile, column block), heaviest tiles first
       tile = nt_all - 1 - tc / gy;
       if (!direct_heavy(tile)) return;

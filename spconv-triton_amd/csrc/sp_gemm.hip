@@ -521,7 +521,8 @@ struct GemmCall {
   const uint32_t* words;  // ordered direct kernel: the rows' mask words (nullable), mic per row
   int mic;
   bool vec;
-  bool thin;             // planned: the thin kernel (tiles of at most kThinItems items)
+  int thin;              // planned: 1 the thin kernel (tiles of at most kThinItems items),
+                         // 2 its quarter instance with every heavy tile split
 };
 
 // Raises a kernel's dynamic LDS limit to `bytes` (once per kernel and process).
@@ -627,7 +628,7 @@ template <typename T, typename OutT, bool VEC>
 static int launch_thin(dim3 grid, hipStream_t s, const T* A, const T* bt, const int32_t* pairs,
                        OutT* o, GemmBufs nb, const GemmCall& c) {
   const uint32_t lds = thin_kernel_lds(c.kv, uint32_t(sizeof(OutT)));
-  const bool quarter = sizeof(T) == 4 || grid.x <= kThinQuarterGrid;
+  const bool quarter = sizeof(T) == 4 || grid.x <= kThinQuarterGrid || c.thin == 2;
   auto kern = quarter ? (c.order ? gather_gemm_thin<T, OutT, VEC, true, true>
                                  : gather_gemm_thin<T, OutT, VEC, false, true>)
                       : (c.order ? gather_gemm_thin<T, OutT, VEC, true, false>
@@ -638,7 +639,12 @@ static int launch_thin(dim3 grid, hipStream_t s, const T* A, const T* bt, const 
                      attr_set[(c.order ? 1 : 0) + (quarter ? 2 : 0)]);
   if (rc) return rc;
   const int64_t nt = cdiv(c.M, kTileRows);
-  const int n_split = quarter ? int(nt < kThinSplitTiles ? nt : kThinSplitTiles) : 0;
+  // thin == 2: every tile the direct path takes is spread over four
+  // workgroups (tables whose tiles mostly hold more items than the thin
+  // layout, with fp32 operands: their waves' MFMAs set the kernel's end)
+  const int n_split = !quarter ? 0
+                      : c.thin == 2 ? int(nt)
+                                    : int(nt < kThinSplitTiles ? nt : kThinSplitTiles);
   const int64_t n_extra = thin_split_extra(n_split, int(cdiv(c.N, 64)));
   SP_CHECK_ARG(n_extra + grid.x <= kMaxGridX, "gemm: too many tiles");
   grid.x = unsigned(n_extra + grid.x);
@@ -717,7 +723,7 @@ static int gemm_packed(const void* A, int dtype, int64_t n_src, const void* pack
                        int64_t kv, int64_t C, int transpose, int has_bias, const int32_t* pairs,
                        int64_t M, const int32_t* pm, const int32_t* ar, const void* plan,
                        size_t plan_bytes, void* out, int out_dtype, hipStream_t s,
-                       const int32_t* order = nullptr, bool thin = false,
+                       const int32_t* order = nullptr, int thin = 0,
                        const uint32_t* words = nullptr, int mic = 0) {
   SP_CHECK_ARG(gemm_dtype_ok(dtype), "gemm: feature dtype %d not supported (f16/bf16/f32)", dtype);
   SP_CHECK_ARG(K >= 1 && C >= 1 && kv >= 1 && M >= 0 && n_src >= 0, "gemm: bad sizes");
@@ -726,6 +732,7 @@ static int gemm_packed(const void* A, int dtype, int64_t n_src, const void* pack
   SP_CHECK_ARG(!(pm && kv > 32), "gemm: masked path needs kv <= 32");
   SP_CHECK_ARG(!words || (order && mic >= (kv + 31) / 32 && mic <= 1024),
                "gemm: row mask words need a row order and >= ceil(kv/32) words per row (%d)", mic);
+  SP_CHECK_ARG(thin >= 0 && thin <= 2, "gemm: thin_tiles must be 0, 1 or 2, not %d", thin);
   if (M == 0) return SP_OK;
   SP_CHECK_ARG(A && packed && pairs && out, "gemm: null pointer");
   const Packed p = packed_layout(K, kv, C, dtype, transpose);
@@ -743,7 +750,7 @@ static int gemm_packed(const void* A, int dtype, int64_t n_src, const void* pack
   c.mic = words ? mic : 0;
   c.vec = (p.R % vec_of(dtype) == 0) && (reinterpret_cast<uintptr_t>(A) % 16 == 0);
   c.planned = plan != nullptr;
-  c.thin = thin && plan != nullptr;
+  c.thin = plan != nullptr ? thin : 0;
   c.plan = PlanDev{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0};
   if (plan) {
     SP_CHECK_ARG(kv <= kPlanMaxKv, "gemm: gather plans need kv <= %d", kPlanMaxKv);
@@ -887,7 +894,7 @@ int sp_conv_gemm_ordered(const void* a, int32_t dtype, int64_t n_src, const void
   SP_CHECK_ARG(row_order != nullptr, "gemm: null row order");
   return gemm_packed(a, dtype, n_src, packed, K, kv, C, transpose, has_bias, pairs_perm, M,
                      nullptr, nullptr, plan, plan_bytes, out, out_dtype, as_stream(stream),
-                     row_order, thin_tiles != 0, row_words, int(words_per_row));
+                     row_order, int(thin_tiles), row_words, int(words_per_row));
 }
 
 int sp_conv_fwd(const void* x, int32_t dtype, int64_t n_in, int64_t C, const void* w,

@@ -240,6 +240,17 @@ SURE_PAIRS_PER_ROW = 1.05
 #: or off (False) for every ordered call ("auto": by that rule).
 THIN_MAX_ITEMS_PER_TILE = 1.5
 THIN_TILES = "auto"
+#: Mask-ordered tables with more items per tile, under IEEE fp32 operands,
+#: run the thin kernel's quarter instance with every tile it hands to the
+#: direct path spread over four workgroups (thin_tiles 2 of
+#: sp_conv_gemm_ordered): the tiles with the most mask bits carry most of the
+#: MFMA work (LiDAR-like 50k cloud: 95 of 196 tiles, 82 % of it), and their
+#: waves set the kernel's end.  GEMM 256 -> 256 603 -> 483 us (staged ->
+#: split), 128 -> 128 229 -> 164 us; for 16-bit operands the staged kernel
+#: stays faster (107 against 179 us), and tables of about one pair per row
+#: keep the thin kernel's last-16-tiles split (splitting every tile measured
+#: 0.101 -> 0.105 ms on the uniform reference-class layer).
+THIN_SPLIT_FP32 = True
 #: kv range of the gather plans (sp_gather_plan_bytes: 1..1024).  A plan tile
 #: holds at most 64 live offsets (more: its rows are gathered directly), so
 #: natural-order tables are planned up to kv = 64 only (a 5^3 window's natural
@@ -496,11 +507,14 @@ def _gemm(a: torch.Tensor, filters: torch.Tensor, bias, transpose: bool, pairs: 
     if variant is not None:
         order, perm, plan = variant
         thin = THIN_TILES if THIN_TILES != "auto" else getattr(perm, "_spconv_triton_thin", False)
+        if (THIN_TILES == "auto" and THIN_SPLIT_FP32 and not thin and plan is not None
+                and a.dtype == torch.float32 and not split):
+            thin = 2  # see THIN_SPLIT_FP32
         words = getattr(perm, "_spconv_triton_words", None)  # sorted mask words [M, mic]
         _lib.check(L.sp_conv_gemm_ordered(
             _lib.ptr(a), _lib.dtype_code(a.dtype), a.shape[0], _lib.ptr(packed), K, kv, C,
             int(transpose), int(bias is not None), _lib.ptr(perm), M, _lib.ptr(order),
-            _lib.ptr(plan), 0 if plan is None else plan.numel(), int(bool(thin)),
+            _lib.ptr(plan), 0 if plan is None else plan.numel(), int(thin),
             _lib.ptr(words), 0 if words is None else words.shape[1], _lib.ptr(out),
             _lib.dtype_code(out.dtype), _lib.stream_of(a.device)), "sp_conv_gemm_ordered")
         return

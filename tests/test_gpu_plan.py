@@ -311,8 +311,9 @@ def test_plan_many_offsets(kv):
 
 
 def _planned_vs_direct(a, w, pairs, M, plan, dtype):
-    """The direct kernel (no plan) and the planned kernels (staged, thin) over
-    a table in its own row order, through the C ABI: [direct, staged, thin]."""
+    """The direct kernel (no plan) and the planned kernels (staged, thin, thin
+    with every heavy tile split over four workgroups) over a table in its own
+    row order, through the C ABI: [direct, staged, thin, split]."""
     from spconv_triton.pytorch._impl import _lib, gemm
 
     L = _lib.lib()
@@ -322,7 +323,7 @@ def _planned_vs_direct(a, w, pairs, M, plan, dtype):
     s = _lib.stream_of(a.device)
     ident = torch.arange(M, dtype=torch.int32, device=DEV)
     outs = []
-    for mode in ("direct", "staged", "thin"):
+    for mode in ("direct", "staged", "thin", "split"):
         out = torch.full((M, K), float("nan"), dtype=dtype, device=DEV)
         if mode == "direct":
             rc = L.sp_conv_gemm_packed(_lib.ptr(a), dt, a.shape[0], _lib.ptr(packed), K, kv, C, 0,
@@ -330,8 +331,9 @@ def _planned_vs_direct(a, w, pairs, M, plan, dtype):
         else:
             rc = L.sp_conv_gemm_ordered(_lib.ptr(a), dt, a.shape[0], _lib.ptr(packed), K, kv, C,
                                         0, 0, _lib.ptr(pairs), M, _lib.ptr(ident),
-                                        _lib.ptr(plan), plan.numel(), int(mode == "thin"), None,
-                                        0, _lib.ptr(out), dt, s)
+                                        _lib.ptr(plan), plan.numel(),
+                                        {"staged": 0, "thin": 1, "split": 2}[mode], None, 0,
+                                        _lib.ptr(out), dt, s)
         _lib.check(rc, mode)
         outs.append(out)
     torch.cuda.synchronize()
@@ -377,10 +379,11 @@ def test_planned_tiles_within_one_offset_group(dtype):
     x, _ = _q(torch.randn(n_src, C), dtype)
     w, _ = _q(torch.randn(K, kv, C) / np.sqrt(kv * C), dtype)
     plan = gemm.gather_plan(pf, n_src)
-    direct, staged, thin = _planned_vs_direct(x, w, pf, M, plan, dtype)
+    direct, staged, thin, split = _planned_vs_direct(x, w, pf, M, plan, dtype)
     assert not torch.isnan(direct).any()
     assert torch.equal(staged, direct), "staged kernel differs from the direct kernel"
     assert torch.equal(thin, direct), "thin kernel differs from the direct kernel"
+    assert torch.equal(split, direct), "thin kernel (every tile split) differs"
 
 
 def test_planned_metric_shape():
@@ -463,12 +466,13 @@ def _orders(a, w, bias, transpose, pairs, M):
     prev = gemm.ROW_ORDER, gemm.USE_GATHER_PLAN, gemm.THIN_TILES
     for mode, use, thin in (("natural", True, "auto"), ("natural", False, "auto"),
                             ("mask", True, False), ("mask", False, "auto"),
-                            ("mask", True, True)):
+                            ("mask", True, True), ("mask", True, 2)):
         gemm.ROW_ORDER, gemm.USE_GATHER_PLAN, gemm.THIN_TILES = mode, use, thin
         try:
             out = torch.empty((M, N), dtype=a.dtype, device=DEV)
             gemm._gemm(a, w, bias, transpose, pairs, M, None, None, out)
-            outs[(mode, use) if thin != True else (mode, use, "thin")] = out  # noqa: E712
+            key = {True: (mode, use, "thin"), 2: (mode, use, "split")}.get(thin, (mode, use))
+            outs[key] = out
         finally:
             gemm.ROW_ORDER, gemm.USE_GATHER_PLAN, gemm.THIN_TILES = prev
     return outs

@@ -96,6 +96,12 @@ def test_workspace_queries_and_bad_geometry():
     bad = _geom(_lib.SP_PAIR_SUBM, [8, 8, 8], [8, 8, 8], ks=2)
     assert L.sp_geom_key64(ctypes.byref(bad)) == -1
     assert b"odd" in L.sp_last_error()
+    # the ordered GEMM's kernel mode is checked before anything runs (M = 0)
+    order = (ctypes.c_int32 * 1)(0)
+    for thin, rc in ((0, 0), (2, 0), (3, _lib.SP_ERR_INVALID_ARG), (-1, _lib.SP_ERR_INVALID_ARG)):
+        assert L.sp_conv_gemm_ordered(None, _lib.SP_F16, 0, None, 8, 27, 8, 0, 0, None, 0, order,
+                                      None, 0, thin, None, 0, None, _lib.SP_F16, None) == rc
+    assert b"thin_tiles" in L.sp_last_error()
 
 
 def test_error_mapping():
