@@ -140,3 +140,50 @@ def test_reference_class_layer_matches_oracle(cloud, kind, dtype):
     ref = orc.gemm_dgrad(gn, wn, pbn)
     s = orc.gemm_dgrad(np.abs(gn), np.abs(wn), pbn) if dtype == "tf32" else None
     _check(dx[torch.from_numpy(rows).to(DEV)], ref, dtype, f"{kind} dgrad", s)
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "fp32", "tf32"])
+def test_lidar_cloud_layer_matches_oracle(dtype):
+    """The same layer (SubMConv3d 256 -> 256, 50k voxels in 41 x 1600 x 1408)
+    on the LiDAR-like cloud of ``bench_data.lidar_cloud`` (3.27 pairs per
+    row).  Its table takes the mask order at the second call: 16-bit operands
+    (fp16, and TF32's split bf16) through the band for sparse tables of 27 or
+    more offsets, run by the staged kernel, whose tiles mostly overflow LDS
+    and take its direct path; fp32 through the per-64-row-block work count,
+    run by the thin kernel with every heavy tile split over four workgroups.
+    Every 7th output row of the forward is compared with the fp64 oracle and
+    the whole output with the natural order's, bit for bit."""
+    from spconv_triton import constants
+    from spconv_triton.core import ConvAlgo
+    from spconv_triton.pytorch import ops
+    from spconv_triton.pytorch._impl import gemm
+
+    from bench_data import lidar_cloud
+
+    print(f"[lidar_c256] {dtype}", flush=True)
+    idx = lidar_cloud(50000, batch=1, seed=0, shape=SHAPE)
+    pf = ops.get_indice_pairs_implicit_gemm(torch.from_numpy(idx).to(DEV), 1, SHAPE,
+                                            ConvAlgo.MaskImplicitGemm, [3] * 3, [1] * 3, [1] * 3,
+                                            [1] * 3, [0] * 3, True, False, is_train=False)[2]
+    kv, n = pf.shape
+    torch.manual_seed(4)
+    x = _operand((n, C), dtype)
+    w = _operand((K, kv, C), dtype, 1.0 / np.sqrt(kv * C))
+    prev = constants.SPCONV_ALLOW_TF32
+    constants.SPCONV_ALLOW_TF32 = dtype == "tf32"
+    try:
+        out = _run(lambda: gemm.conv_forward(x, w, pf, n), pf, False, "forward")
+        variant = pf._spconv_triton_order[1]
+        assert isinstance(variant, tuple) and variant[2] is not None, \
+            "the planned mask order was not taken"
+        assert not getattr(variant[1], "_spconv_triton_thin", False)
+        nat = _natural(lambda: gemm.conv_forward(x, w, pf.clone(), n))
+    finally:
+        constants.SPCONV_ALLOW_TF32 = prev
+    assert torch.equal(out, nat), "forward: mask order != natural order"
+    rows = np.arange(0, n, EVERY)
+    xn, wn = (t.double().cpu().numpy() for t in (x, w))
+    pfn = pf.cpu().numpy()[:, rows]
+    ref = orc.gemm_fwd(xn, wn, pfn)
+    s = orc.gemm_fwd(np.abs(xn), np.abs(wn), pfn) if dtype == "tf32" else None
+    _check(out[torch.from_numpy(rows).to(DEV)], ref, dtype, "forward", s)
