@@ -64,7 +64,7 @@ constexpr int kGroupOffsets = 64;          // kernel offsets per group (direct k
 static_assert(kGroupOffsets == kPlanGroupOffsets,
               "planned tiles keep their items in one group of the direct kernel");
 constexpr uint32_t kSlabBytes = 4096;      // B of one item: 4 pieces x 64 columns x 16 B
-constexpr int kPad = 7;                    // padding items after a direct-kernel item list
+constexpr int kPad = 5;                    // padding items after a direct-kernel item list
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   // word 3 = 0x00020000: 32-bit data format, the raw-buffer setting for gfx9 parts
@@ -315,14 +315,15 @@ __device__ __forceinline__ void store_tile(const floatx16 (&acc)[2][2], const fl
 // Dynamic LDS of the direct kernel: per wave E item entries; the epilogue
 // tiles overlap the tables (used after the last item).
 struct DirectLds {
-  uint32_t kb_off, src_off, total;
+  uint32_t kb_off, src_off, a_off, total;
 };
 
 __host__ __device__ inline DirectLds direct_lds(int E, uint32_t out_size) {
   DirectLds l;
   l.kb_off = 0;                                          // uint32 B offsets [4][E]
   l.src_off = (16u * uint32_t(E) + 255u) / 256u * 256u;  // int32 source rows [4][E][32][2]
-  l.total = l.src_off + uint32_t(E) * 1024u;
+  l.a_off = l.src_off + uint32_t(E) * 1024u;             // direct_tile's A slots [4][32][64 B]
+  l.total = l.a_off + 4u * 2048u;
   if (l.total < l.src_off + epi_bytes(out_size)) l.total = l.src_off + epi_bytes(out_size);
   return l;
 }
@@ -334,7 +335,7 @@ __host__ __device__ inline DirectLds direct_lds(int E, uint32_t out_size) {
 // row (bit k of row r set iff pairs[k, r] >= 0); with them a wave reads the
 // table entries of only the offsets set in its rows' masks, instead of all kv
 // (the items found, and so the result, are the same).
-template <typename T, typename OutT, bool VEC>
+template <typename T, typename OutT, bool VEC, bool SLOT = true>
 __device__ __forceinline__ void direct_tile(const T* __restrict__ A, const T* __restrict__ Bt,
                                             const int32_t* __restrict__ pairs,
                                             const float* __restrict__ bias,
@@ -493,6 +494,125 @@ __device__ __forceinline__ void direct_tile(const T* __restrict__ A, const T* __
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) b[ks][nt] = buf_frag<T>(rb, kr + bl[ks][nt]);
     };
+    if constexpr (VEC && SLOT) {
+      // A through a wave-private LDS slot.  A gather fragment (lane l: row
+      // l % 32, piece 2 ks + l / 32) reads 32 rows, 32 of their 64 bytes
+      // each, and costs the L1 one tag per row; loaded row-contiguous
+      // instead (lane l: row 16 ks + l / 4, piece l % 4: each load 16 whole
+      // 64-byte rows) a step's 64 rows take half the tags.  The loads land in
+      // registers, go through the slot (rows swizzled as in the staged
+      // kernel) a step later, one 32-row block at a time, and come back as
+      // the same MFMA fragments: the multiply and its result are unchanged.
+      // LDS operations of one wave complete in order, so one slot serves
+      // every block and step.  (A timing probe of the loads alone: the
+      // unplanned 4-D 3^4 layer 273 -> 221 us.)
+      unsigned char* aslot = smem + L.a_off + uint32_t(wave) * 2048u;
+      const int rsub = lane >> 2, pc = lane & 3;  // this lane's row (within 16) and piece
+      const int last_it = nact + kPad - 1;        // the cursors' reads stop at the last padding item
+      // byte offsets in A of this lane's four rows (16 ks + rsub of block mt)
+      auto bases = [&](int it) -> uint4 {
+        const int i = it < last_it ? it : last_it;
+        const uint2 r0 = *reinterpret_cast<const uint2*>(s_src + (i * 32 + rsub) * 2);
+        const uint2 r1 = *reinterpret_cast<const uint2*>(s_src + (i * 32 + 16 + rsub) * 2);
+        return make_uint4(r0.x, r0.y, r1.x, r1.y);  // [ks][mt]
+      };
+      auto gload_a = [&](const uint4& bs, int rc, uint4 (&raw)[2][2]) {
+        const int e0 = rc * kChunk + pc * V;
+        const uint32_t b4[2][2] = {{bs.x, bs.y}, {bs.z, bs.w}};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt) {
+            const uint32_t base = b4[ks][mt];
+            raw[ks][mt] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                           ra, (base != kOob && e0 < R) ? base + uint32_t(e0) * ES : kOob, 0, 0));
+          }
+      };
+      // row r of the slot at chunk_base(r), its piece p at ^ (p << 4)
+      const uint32_t wr_row = chunk_base(uint32_t(rsub)) ^ uint32_t(pc << 4);
+      const uint32_t rd_row = chunk_base(uint32_t(l32));
+      auto through_slot = [&](const uint4 (&raw)[2][2], frag (&a)[2][2]) {
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks)  // rows 16 ks .. 16 ks + 15 (chunk_base(r + 16) = + 1024)
+            *reinterpret_cast<uint4*>(aslot + wr_row + uint32_t(ks) * 1024u) = raw[ks][mt];
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks)
+            a[ks][mt] = *reinterpret_cast<const frag*>(aslot +
+                                                       (rd_row ^ uint32_t((ks * 2 + h) << 4)));
+        }
+      };
+      frag b0[2][2], b1[2][2], b2[2][2], b3[2][2], a0[2][2], a1[2][2];
+      uint4 q0[2][2], q1[2][2];  // row-contiguous A loads of a step
+      Cur ca{0, 0}, cb{0, 0};    // the steps of the next A bases and the next B loads
+      uint4 e_cur;               // bases of the next A loads' step
+      int rc_cur;
+      {
+        const uint32_t k0 = s_kb[0];
+        const int rc0 = cb.rc;
+        advance(cb);
+        const uint32_t k1 = s_kb[cb.it];
+        const int rc1 = cb.rc;
+        advance(cb);
+        const uint4 e0 = bases(ca.it);
+        const int ra0 = ca.rc;
+        advance(ca);
+        const uint4 e1 = bases(ca.it);
+        const int ra1 = ca.rc;
+        advance(ca);
+        e_cur = bases(ca.it);
+        rc_cur = ca.rc;
+        advance(ca);
+        __builtin_amdgcn_sched_barrier(0);
+        gload_a(e0, ra0, q0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(k0, rc0, b0);
+        __builtin_amdgcn_sched_barrier(0);
+        gload_a(e1, ra1, q1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(k1, rc1, b1);
+        __builtin_amdgcn_sched_barrier(0);
+        through_slot(q0, a0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // Step j: the A loads of step j + 2 (their bases read in step j - 1),
+      // the MFMAs of step j (fragments from step j - 1), the fragments of
+      // step j + 1 through the slot (loaded in step j - 1), the B loads of
+      // step j + 2 and the A bases of step j + 3.
+      auto step = [&](frag (&bc)[2][2], frag (&bn)[2][2], frag (&ac)[2][2], frag (&an)[2][2],
+                      uint4 (&qn1)[2][2], uint4 (&qn2)[2][2]) {
+        const uint32_t kb = s_kb[cb.it];
+        const int rcb = cb.rc;
+        advance(cb);
+        gload_a(e_cur, rc_cur, qn2);
+        const uint4 e_nxt = bases(ca.it);
+        const int rc_nxt = ca.rc;
+        advance(ca);
+        __builtin_amdgcn_sched_barrier(0);
+        mma_item<T>(ac, bc, acc);
+        __builtin_amdgcn_sched_barrier(0);
+        through_slot(qn1, an);
+        __builtin_amdgcn_sched_barrier(0);
+        load_b(kb, rcb, bn);
+        __builtin_amdgcn_sched_barrier(0);
+        e_cur = e_nxt;
+        rc_cur = rc_nxt;
+      };
+      // Steps 0 .. 4 ceil(S / 4) - 1 for S = nrc * nact: the A and B loads
+      // reach at most item nact + 4 of the last chunk, the last padding item
+      // (the bases read ahead stop there).
+      static_assert(kPad >= 5, "the loads run 4 items past the last one");
+      const int n_steps = nrc * nact;
+      for (int j = 0; j < n_steps; j += 4) {
+        step(b0, b2, a0, a1, q1, q0);
+        step(b1, b3, a1, a0, q0, q1);
+        step(b2, b0, a0, a1, q1, q0);
+        step(b3, b1, a1, a0, q0, q1);
+      }
+      continue;
+    }
     auto load_a = [&](const uint2& e, int rc, frag (&a)[2][2]) {
       const uint32_t s2[2] = {e.x, e.y};
 #pragma unroll
@@ -874,8 +994,11 @@ __global__ __launch_bounds__(256, 2) void gather_gemm_staged(
   const int nact = plan.nact[tile];
   const int32_t ko = tid < E ? plan.koff[tile * E + tid] : -1;
   if (U >= kLdsRows) {  // whole workgroup: an overflow tile
-    direct_tile<T, OutT, VEC>(A, Bt, pairs, bias, out, nb, n_src, M, N, R, Rp, kv, tile, n0, smem,
-                              order);
+    // (the natural-order instances, whose tiles rarely overflow, keep the
+    // gathers straight into fragments: the slot path's registers cost the
+    // metric layer's staged steps 0.8 us)
+    direct_tile<T, OutT, VEC, ORDERED>(A, Bt, pairs, bias, out, nb, n_src, M, N, R, Rp, kv, tile,
+                                       n0, smem, order);
     return;
   }
   // byte offsets of the rows in A, kept in LDS (not registers) while the
