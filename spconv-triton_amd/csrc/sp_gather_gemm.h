@@ -494,8 +494,10 @@ __device__ __forceinline__ void direct_tile(const T* __restrict__ A, const T* __
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) b[ks][nt] = buf_frag<T>(rb, kr + bl[ks][nt]);
     };
-    if constexpr (VEC && SLOT) {
-      // A through a wave-private LDS slot.  A gather fragment (lane l: row
+    if constexpr (VEC && SLOT && sizeof(T) == 2) {
+      // A through a wave-private LDS slot (16-bit operands: with fp32 ones,
+      // whose 64-clock MFMAs leave the gathers more time, it measured slower:
+      // the LiDAR-like layer's mask-ordered direct GEMM 1 132 -> 1 250 us).  A gather fragment (lane l: row
       // l % 32, piece 2 ks + l / 32) reads 32 rows, 32 of their 64 bytes
       // each, and costs the L1 one tag per row; loaded row-contiguous
       // instead (lane l: row 16 ks + l / 4, piece l % 4: each load 16 whole
